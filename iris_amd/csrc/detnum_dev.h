@@ -1,0 +1,337 @@
+// Device-side det-num: the fixed-point arithmetic of crates/det-num restated
+// for gfx950. Every function returns the same bits as the reference function
+// it names; where operand ranges allow, the 128-bit steps are narrowed to
+// 64-bit ones that give the identical result (the narrowing is noted).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dn {
+
+typedef __int128 i128;
+typedef unsigned __int128 u128;
+
+constexpr int32_t ONE_ACT = 1 << 16;
+constexpr int64_t ONE_ACC = (int64_t)1 << 32;
+
+__device__ __forceinline__ int32_t clamp_i64_to_i32(int64_t v) {
+    return v < INT32_MIN ? INT32_MIN : (v > INT32_MAX ? INT32_MAX : (int32_t)v);
+}
+__device__ __forceinline__ int32_t clamp_i128_to_i32(i128 v) {
+    return v < (i128)INT32_MIN ? INT32_MIN : (v > (i128)INT32_MAX ? INT32_MAX : (int32_t)v);
+}
+__device__ __forceinline__ int64_t clamp_i128_to_i64(i128 v) {
+    return v < (i128)INT64_MIN ? INT64_MIN : (v > (i128)INT64_MAX ? INT64_MAX : (int64_t)v);
+}
+__device__ __forceinline__ int32_t sat_neg_i32(int32_t v) { return v == INT32_MIN ? INT32_MAX : -v; }
+__device__ __forceinline__ int64_t sat_neg_i64(int64_t v) { return v == INT64_MIN ? INT64_MAX : -v; }
+
+// ops.rs:773-803. Round-half-even of x / 2^shift; the floor form below is the
+// same rounding as the reference's truncate-then-step form.
+__device__ __forceinline__ int64_t rshift_rte(int64_t x, uint32_t shift) {
+    if (shift == 0) return x;
+    int64_t fl = x >> shift;
+    uint64_t rem = (uint64_t)x & ((((uint64_t)1) << shift) - 1);
+    uint64_t half = (uint64_t)1 << (shift - 1);
+    return (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+}
+
+// ops.rs:448-451 + :483-486
+__device__ __forceinline__ int32_t requantize(int64_t acc) { return clamp_i64_to_i32(rshift_rte(acc, 16)); }
+// ops.rs:41-45
+__device__ __forceinline__ int32_t mul_sat(int32_t a, int32_t b) { return requantize((int64_t)a * (int64_t)b); }
+// ops.rs:36-38, :431-433
+__device__ __forceinline__ int32_t add_sat(int32_t a, int32_t b) { return clamp_i64_to_i32((int64_t)a + b); }
+__device__ __forceinline__ int32_t sub_sat(int32_t a, int32_t b) { return clamp_i64_to_i32((int64_t)a - b); }
+// ops.rs:436-438
+__device__ __forceinline__ int64_t acc_add_sat(int64_t a, int64_t b) {
+    int64_t s;
+    if (__builtin_add_overflow(a, b, &s)) return a < 0 ? INT64_MIN : INT64_MAX;
+    return s;
+}
+
+// ops.rs:691-720 on 64-bit operands (the callers below never exceed them).
+__device__ __forceinline__ int64_t rte_div_i64(int64_t dividend, int64_t divisor) {
+    int64_t q = dividend / divisor;
+    int64_t r = dividend % divisor;
+    if (r == 0) return q;
+    uint64_t twice = (uint64_t)(r < 0 ? -r : r) * 2;
+    uint64_t absd = (uint64_t)(divisor < 0 ? -divisor : divisor);
+    int64_t step = ((dividend < 0) != (divisor < 0)) ? -1 : 1;
+    if (twice < absd) return q;
+    if (twice > absd) return q + step;
+    return (q & 1) == 0 ? q : q + step;
+}
+
+// ops.rs:691-720, full width.
+__device__ __forceinline__ i128 rte_div_i128(i128 dividend, i128 divisor) {
+    i128 q = dividend / divisor;
+    i128 r = dividend % divisor;
+    if (r == 0) return q;
+    i128 twice = (r < 0 ? -r : r) * 2;
+    i128 absd = divisor < 0 ? -divisor : divisor;
+    i128 step = ((dividend < 0) != (divisor < 0)) ? -1 : 1;
+    if (twice < absd) return q;
+    if (twice > absd) return q + step;
+    return (q & 1) == 0 ? q : q + step;
+}
+
+// ops.rs:81-88: an i64 over a u32 never needs more than 64 bits.
+__device__ __forceinline__ int64_t div_acc_by_u32(int64_t value, uint32_t divisor) {
+    return rte_div_i64(value, (int64_t)divisor);
+}
+
+// ops.rs:53-64: (n << 16) fits in 48 bits.
+__device__ __forceinline__ int32_t div_act(int32_t n, int32_t d) {
+    return clamp_i64_to_i32(rte_div_i64((int64_t)n * 65536, (int64_t)d));
+}
+
+// ops.rs:685-689: round-half-even of a*b / 2^32, clamped.
+__device__ __forceinline__ int64_t acc_mul(int64_t a, int64_t b) {
+    i128 p = (i128)a * (i128)b;
+    i128 fl = p >> 32;
+    uint64_t rem = (uint64_t)p & 0xffffffffull;
+    const uint64_t half = 0x80000000ull;
+    i128 r = (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+    return clamp_i128_to_i64(r);
+}
+
+// ops.rs:67-78 div_acc for the softmax's case: numerator in [0, 2^32] and
+// denominator >= numerator > 0, so the 96-bit dividend e * 2^32 <= 2^64 is
+// handled with one 64-bit division (the 2^64 edge by its predecessor).
+__device__ __forceinline__ int64_t div_acc_softmax(uint64_t e, uint64_t sum) {
+    uint64_t q, r;
+    if (e < ((uint64_t)1 << 32)) {
+        uint64_t d = e << 32;
+        q = d / sum;
+        r = d - q * sum;
+    } else {  // e == 2^32: dividend 2^64 = (2^64 - 1) + 1
+        uint64_t d = ~(uint64_t)0;
+        q = d / sum;
+        r = d - q * sum + 1;
+        if (r == sum) { q += 1; r = 0; }
+    }
+    if (r == 0) return (int64_t)q;
+    // twice-remainder against the divisor, without overflow
+    uint64_t other = sum - r;
+    if (r < other) return (int64_t)q;
+    if (r > other) return (int64_t)(q + 1);
+    return (q & 1) == 0 ? (int64_t)q : (int64_t)(q + 1);
+}
+
+// ops.rs:722-771
+__device__ inline int32_t inv_sqrt_acc(int64_t x) {
+    if (x == 0) return INT32_MAX;
+    const u128 target = (u128)1 << 64;
+    const u128 divisor = (u128)(uint64_t)x;
+    const uint32_t max_bits = (uint32_t)INT32_MAX;
+    auto prod = [&](uint32_t c) -> u128 { return (u128)((uint64_t)c * (uint64_t)c) * divisor; };
+    if (prod(max_bits) <= target) return INT32_MAX;
+    uint32_t low = 0, high = max_bits;
+    while (low < high) {
+        uint32_t mid = low + ((high - low + 1) >> 1);
+        if (prod(mid) <= target) low = mid;
+        else high = mid - 1;
+    }
+    uint32_t lower = low;
+    uint32_t upper = lower + 1 > max_bits ? max_bits : lower + 1;
+    u128 le = target - prod(lower);
+    u128 up = prod(upper);
+    u128 ue = up > target ? up - target : 0;
+    uint32_t r;
+    if (upper == lower || le < ue) r = lower;
+    else if (ue < le) r = upper;
+    else r = (lower & 1) == 0 ? lower : upper;
+    return (int32_t)r;
+}
+
+// ops.rs:409-428 after the (order-free, saturating) sum of squares.
+__device__ __forceinline__ int32_t rms_scale_from_sum(int64_t sum_squares, uint32_t n, int64_t eps) {
+    int64_t mean = div_acc_by_u32(sum_squares, n);
+    return inv_sqrt_acc(acc_add_sat(mean, eps));
+}
+
+// ops.rs:508-556
+__device__ inline int64_t softmax_exp_term(int64_t delta) {
+    const int64_t LN_2_BITS = 2977044472LL;
+    const int64_t MIN_DELTA = -((int64_t)16 << 32);
+    if (delta <= MIN_DELTA) return 0;
+    int64_t positive = sat_neg_i64(delta);
+    int64_t shift = positive / LN_2_BITS;
+    int64_t r = positive % LN_2_BITS;
+    int64_t r2 = acc_mul(r, r);
+    int64_t r3 = acc_mul(r2, r);
+    int64_t r4 = acc_mul(r3, r);
+    int64_t r5 = acc_mul(r4, r);
+    int64_t approx = acc_add_sat(
+        acc_add_sat(ONE_ACC, sat_neg_i64(r)),
+        acc_add_sat(div_acc_by_u32(r2, 2),
+                    acc_add_sat(sat_neg_i64(div_acc_by_u32(r3, 6)),
+                                acc_add_sat(div_acc_by_u32(r4, 24), sat_neg_i64(div_acc_by_u32(r5, 120))))));
+    if (approx <= 0) return 0;
+    if (shift < 64) return rshift_rte(approx, (uint32_t)shift);
+    return 0;
+}
+
+// ops.rs:357-377
+__device__ inline int32_t tanh_act(int32_t x) {
+    const int32_t LIN = 27 << 16, QUAD = 9 << 16, SAT = 3 << 16;
+    if (x >= SAT) return ONE_ACT;
+    if (x <= -SAT) return -ONE_ACT;
+    int32_t x2 = mul_sat(x, x);
+    int32_t num_scale = add_sat(LIN, x2);
+    int32_t den_scale = add_sat(LIN, mul_sat(QUAD, x2));
+    return div_act(mul_sat(x, num_scale), den_scale);
+}
+
+// ops.rs:380-388 (with sequence-check's cap <= 0 passthrough)
+__device__ inline int32_t softcap(int32_t x, int32_t cap) {
+    if (cap <= 0) return x;
+    return mul_sat(cap, tanh_act(div_act(x, cap)));
+}
+
+// ops.rs:391-406
+__device__ inline int32_t gelu(int32_t x) {
+    int32_t x2 = mul_sat(x, x);
+    int32_t x3 = mul_sat(x2, x);
+    int32_t inner = add_sat(x, mul_sat(2930, x3));
+    int32_t t = tanh_act(mul_sat(52290, inner));
+    return mul_sat(mul_sat(1 << 15, x), add_sat(ONE_ACT, t));
+}
+
+__device__ __forceinline__ int64_t rem_euclid(int64_t a, int64_t m) {
+    int64_t r = a % m;
+    return r < 0 ? r + m : r;
+}
+
+// ops.rs:622-683 sin_cos_acc (returns cos, sin)
+__device__ inline void sin_cos_acc(int64_t angle, int32_t& cos_out, int32_t& sin_out) {
+    const int64_t HALF_PI = 6746518852LL, PI = 13493037705LL, THREE_HALF_PI = 20239556557LL,
+                  TWO_PI = 26986075409LL;
+    int64_t reduced = rem_euclid(angle, TWO_PI);
+    int64_t x;
+    bool sneg = false, cneg = false;
+    if (reduced <= HALF_PI) { x = reduced; }
+    else if (reduced <= PI) { x = PI - reduced; cneg = true; }
+    else if (reduced <= THREE_HALF_PI) { x = reduced - PI; sneg = true; cneg = true; }
+    else { x = TWO_PI - reduced; sneg = true; }
+    int64_t x2 = acc_mul(x, x);
+    int64_t x3 = acc_mul(x2, x);
+    int64_t x5 = acc_mul(x3, x2);
+    int64_t x7 = acc_mul(x5, x2);
+    int64_t sp = acc_add_sat(acc_add_sat(x, sat_neg_i64(div_acc_by_u32(x3, 6))),
+                             acc_add_sat(div_acc_by_u32(x5, 120), sat_neg_i64(div_acc_by_u32(x7, 5040))));
+    int64_t x4 = acc_mul(x2, x2);
+    int64_t x6 = acc_mul(x4, x2);
+    int64_t cp = acc_add_sat(acc_add_sat(ONE_ACC, sat_neg_i64(div_acc_by_u32(x2, 2))),
+                             acc_add_sat(div_acc_by_u32(x4, 24), sat_neg_i64(div_acc_by_u32(x6, 720))));
+    int32_t s = requantize(sp), c = requantize(cp);
+    sin_out = sneg ? sat_neg_i32(s) : s;
+    cos_out = cneg ? sat_neg_i32(c) : c;
+}
+
+// ---- mistral-dense (crates/det-num/src/mistral.rs) ----
+
+// mistral.rs:23-32
+__device__ __forceinline__ int64_t m_shift_rte(int64_t value, uint32_t shift) {
+    int64_t fl = value >> shift;
+    int64_t rem = value - (int64_t)((uint64_t)fl << shift);
+    int64_t half = (int64_t)1 << (shift - 1);
+    return (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+}
+
+// mistral.rs:43-56
+__device__ inline uint64_t exp_neg_q32(uint64_t a) {
+    const uint64_t ONE_Q32 = (uint64_t)1 << 32, LN2 = 2977044472ULL;
+    uint64_t k = a / LN2;
+    if (k >= 32) return 0;
+    uint64_t r = a - k * LN2;
+    uint64_t acc = ONE_Q32;
+#pragma unroll
+    for (uint32_t n = 14; n >= 1; n--) acc = ONE_Q32 - ((r * acc) >> 32) / n;
+    return acc >> k;
+}
+
+// mistral.rs:59-77
+__device__ inline int32_t silu(int32_t x) {
+    const uint64_t ONE_Q32 = (uint64_t)1 << 32;
+    uint64_t mag = x < 0 ? (uint64_t)(-(int64_t)x) : (uint64_t)x;
+    uint64_t divisor = ONE_Q32 + exp_neg_q32(mag << 16);
+    uint64_t positive = (((uint64_t)1 << 63) / divisor) << 1;
+    uint64_t sig = x < 0 ? ONE_Q32 - positive : positive;
+    int64_t product = (int64_t)x * (int64_t)sig;
+    return clamp_i64_to_i32(m_shift_rte(product, 32));
+}
+
+// mistral.rs:84-109 (returns sin, cos in Q30)
+__device__ inline void sin_cos_q30(int64_t angle, int64_t& sin_out, int64_t& cos_out) {
+    const int64_t ONE_Q30 = (int64_t)1 << 30;
+    const int64_t HALF_PI = 6746518852LL, PI = 13493037705LL, THREE_HALF_PI = 20239556557LL,
+                  TWO_PI = 26986075409LL;
+    int64_t reduced = rem_euclid(angle, TWO_PI);
+    int64_t quarter, ss = 1, cs = 1;
+    if (reduced <= HALF_PI) { quarter = reduced; }
+    else if (reduced <= PI) { quarter = PI - reduced; cs = -1; }
+    else if (reduced <= THREE_HALF_PI) { quarter = reduced - PI; ss = -1; cs = -1; }
+    else { quarter = TWO_PI - reduced; ss = -1; }
+    int64_t t = quarter >> 2;
+    int64_t u = (t * t) >> 30;
+    int64_t s = ONE_Q30;
+    s = ONE_Q30 - ((u * s) >> 30) / 210;
+    s = ONE_Q30 - ((u * s) >> 30) / 156;
+    s = ONE_Q30 - ((u * s) >> 30) / 110;
+    s = ONE_Q30 - ((u * s) >> 30) / 72;
+    s = ONE_Q30 - ((u * s) >> 30) / 42;
+    s = ONE_Q30 - ((u * s) >> 30) / 20;
+    s = ONE_Q30 - ((u * s) >> 30) / 6;
+    s = (t * s) >> 30;
+    int64_t c = ONE_Q30;
+    c = ONE_Q30 - ((u * c) >> 30) / 240;
+    c = ONE_Q30 - ((u * c) >> 30) / 182;
+    c = ONE_Q30 - ((u * c) >> 30) / 132;
+    c = ONE_Q30 - ((u * c) >> 30) / 90;
+    c = ONE_Q30 - ((u * c) >> 30) / 56;
+    c = ONE_Q30 - ((u * c) >> 30) / 30;
+    c = ONE_Q30 - ((u * c) >> 30) / 12;
+    c = ONE_Q30 - ((u * c) >> 30) / 2;
+    sin_out = ss * s;
+    cos_out = cs * c;
+}
+
+// mistral.rs:114-126 for one pair (a, b) at angle position * f.
+__device__ __forceinline__ void rotate_pair_q30(int32_t& a, int32_t& b, int64_t angle) {
+    int64_t s, c;
+    sin_cos_q30(angle, s, c);
+    int64_t x = a, y = b;
+    a = clamp_i64_to_i32(m_shift_rte(x * c - y * s, 30));
+    b = clamp_i64_to_i32(m_shift_rte(x * s + y * c, 30));
+}
+
+// mistral.rs:130-145 after the wrapping sum.
+__device__ __forceinline__ int32_t scaled_score_from_sum(int64_t sum, uint32_t scale_q32) {
+    i128 scaled = ((i128)sum * (i128)scale_q32) >> 32;
+    i128 fl = scaled >> 16;
+    int64_t rem = (int64_t)(scaled - (fl << 16));
+    i128 r = (rem > 32768 || (rem == 32768 && (fl & 1))) ? fl + 1 : fl;
+    return clamp_i128_to_i32(r);
+}
+
+// q8.rs:94-104: value / 2^shift, ties to even, saturated to i32.
+__device__ __forceinline__ int32_t round_to_i32(i128 value, uint32_t shift) {
+    i128 fl = value >> shift;
+    i128 rem = value - (fl << shift);
+    i128 half = (i128)1 << (shift - 1);
+    i128 r = (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+    return clamp_i128_to_i32(r);
+}
+
+// q8.rs:27-42: exact Q.24 of finite f16 bits (callers reject exponent 0x1f).
+__device__ __forceinline__ int64_t scale_q24(uint32_t bits) {
+    uint32_t e = (bits >> 10) & 0x1f;
+    int64_t m = bits & 0x3ff;
+    int64_t mag = e == 0 ? m : ((1024 + m) << (e - 1));
+    return (bits & 0x8000) ? -mag : mag;
+}
+
+}  // namespace dn

@@ -1,0 +1,263 @@
+// Exact Q8_0 products on gfx950: the tile packing of an uploaded matrix and
+// the bandwidth-bound product kernel (decode GEMV; also any token count).
+//
+// Every output is det_num::q8::dot_row (crates/det-num/src/q8.rs:56-72):
+// exact block sums, each times the block's Q.24 scale, summed without
+// overflow, rounded once (ties to even) and saturated.
+//
+// Activations are staged in LDS as signed byte digits: a Q16.16 value v is
+// sum_l d_l * 256^l with d_l in [-128, 127], taken as the bytes of
+// v + 0x8080808080 each xor 0x80. The representation is unique, so the digits
+// do not depend on how many are kept; a chunk keeps as many as its largest
+// value needs (1 to 5). Each digit plane times the int8 weights is an exact
+// v_dot4_i32_i8 sum (|sum| < 2^19 per block), and the planes recombine into
+// the exact 64-bit block sum.
+#include "detnum_dev.h"
+#include "q8_internal.h"
+
+namespace {
+
+constexpr int KC_BLOCKS = 128;            // blocks staged per chunk (4096 values)
+constexpr int KC_WORDS = KC_BLOCKS * 8;   // dwords per digit plane per chunk
+constexpr int MAX_LIMBS = 5;
+constexpr int GEMV_WAVES = 8;             // waves per workgroup
+constexpr int GEMV_THREADS = GEMV_WAVES * 64;
+
+__device__ __forceinline__ uint64_t digits5(int32_t v) {
+    return (uint64_t)((int64_t)v + 0x8080808080LL) ^ 0x8080808080ULL;
+}
+
+__device__ __forceinline__ int limbs_needed(uint64_t d) {
+    return (d >> 32) ? 5 : (d >> 24) ? 4 : (d >> 16) ? 3 : (d >> 8) ? 2 : 1;
+}
+
+__device__ __forceinline__ int64_t wave_sum_sat_nonneg(int64_t v) {
+    // Saturating sum of non-negative terms: min(true sum, i64::MAX) in any order.
+    for (int off = 32; off >= 1; off >>= 1) v = dn::acc_add_sat(v, __shfl_xor(v, off));
+    return v;
+}
+
+// Sum of the four kgroups (lanes r, r+16, r+32, r+48) of a wave.
+__device__ __forceinline__ dn::i128 kgroup_sum(dn::i128 v) {
+    for (int off = 16; off <= 32; off <<= 1) {
+        uint64_t lo = (uint64_t)v, hi = (uint64_t)(v >> 64);
+        uint64_t olo = __shfl_xor(lo, off), ohi = __shfl_xor(hi, off);
+        v += (dn::i128)(((dn::u128)ohi << 64) | olo);
+    }
+    return v;
+}
+
+template <int L>
+__device__ __forceinline__ int64_t block_sum(const uint4 q0, const uint4 q1, const uint32_t* lb) {
+    int64_t bs = 0;
+#pragma unroll
+    for (int l = 0; l < L; l++) {
+        const uint32_t* p = lb + l * KC_WORDS;
+        int s = 0;
+        s = __builtin_amdgcn_sdot4((int)q0.x, (int)p[0], s, false);
+        s = __builtin_amdgcn_sdot4((int)q0.y, (int)p[1], s, false);
+        s = __builtin_amdgcn_sdot4((int)q0.z, (int)p[2], s, false);
+        s = __builtin_amdgcn_sdot4((int)q0.w, (int)p[3], s, false);
+        s = __builtin_amdgcn_sdot4((int)q1.x, (int)p[4], s, false);
+        s = __builtin_amdgcn_sdot4((int)q1.y, (int)p[5], s, false);
+        s = __builtin_amdgcn_sdot4((int)q1.z, (int)p[6], s, false);
+        s = __builtin_amdgcn_sdot4((int)q1.w, (int)p[7], s, false);
+        bs += (int64_t)s << (8 * l);
+    }
+    return bs;
+}
+
+// The blocks of one chunk this lane owns, accumulated into acc (i64 sum of
+// block sums in row-scale mode, exact 128-bit sum of scaled block sums else).
+template <int L, int MODE>
+__device__ __forceinline__ void chunk_blocks(const Q8View& w, uint32_t tile, uint32_t cb0, uint32_t cb1,
+                                             uint32_t slot, uint32_t r, const uint32_t* lds, int64_t& acc64,
+                                             dn::i128& acc128) {
+    const uint8_t* qrow = w.qs + (size_t)tile * w.nb * Q8_TILE_BLOCK_BYTES + r * 16;
+    const size_t sbase = (size_t)tile * w.nb * Q8_TILE_ROWS + r;
+    for (uint32_t b = cb0 + slot; b < cb1; b += 4 * GEMV_WAVES) {
+        const uint8_t* qp = qrow + (size_t)b * Q8_TILE_BLOCK_BYTES;
+        const uint4 q0 = *(const uint4*)qp;
+        const uint4 q1 = *(const uint4*)(qp + 256);
+        const int64_t bs = block_sum<L>(q0, q1, lds + (b - cb0) * 8);
+        if constexpr (MODE == Q8_SCALE_ROW) {
+            acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
+        } else if constexpr (MODE == Q8_SCALE_F16) {
+            const uint32_t bits = w.sc16[sbase + (size_t)b * Q8_TILE_ROWS];
+            const uint32_t e = (bits >> 10) & 0x1f;
+            const int64_t m = (int64_t)(bits & 0x3ff) | (e ? 1024 : 0);
+            int64_t p = bs * m;  // < 2^55
+            if (bits & 0x8000) p = -p;
+            acc128 += (dn::i128)p << (e ? e - 1 : 0);
+        } else {
+            acc128 += (dn::i128)bs * (dn::i128)w.sc64[sbase + (size_t)b * Q8_TILE_ROWS];
+        }
+    }
+}
+
+template <int MODE>
+__global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a) {
+    __shared__ uint32_t lds[MAX_LIMBS * KC_WORDS];
+    __shared__ dn::i128 red[GEMV_WAVES][Q8_TILE_ROWS];
+    __shared__ int64_t ssq[GEMV_WAVES];
+    __shared__ int32_t s_scale;
+    __shared__ int s_limbs;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
+    const uint32_t r = lane & 15, g = lane >> 4;
+    const uint32_t slot = wave * 4 + g;
+    const uint32_t tile = blockIdx.x;
+    const uint32_t token = blockIdx.y;
+    const Q8View& w = a.w;
+    const uint32_t K = w.cols;
+    const int32_t* x = a.x + (size_t)token * a.x_stride;
+
+    int32_t scale = 0;
+    if (a.prologue == PRO_RMSNORM) {
+        int64_t s = 0;
+        for (uint32_t k = tid; k < K; k += GEMV_THREADS) s = dn::acc_add_sat(s, (int64_t)x[k] * x[k]);
+        s = wave_sum_sat_nonneg(s);
+        if (lane == 0) ssq[wave] = s;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t t = 0;
+            for (int i = 0; i < GEMV_WAVES; i++) t = dn::acc_add_sat(t, ssq[i]);
+            s_scale = dn::rms_scale_from_sum(t, K, a.norm_eps);
+        }
+        __syncthreads();
+        scale = s_scale;
+    }
+
+    int64_t acc64 = 0;
+    dn::i128 acc128 = 0;
+    for (uint32_t cb0 = 0; cb0 < w.nb; cb0 += KC_BLOCKS) {
+        const uint32_t cb1 = min(cb0 + KC_BLOCKS, w.nb);
+        if (tid == 0) s_limbs = 1;
+        __syncthreads();  // also: the previous chunk's readers are done
+        int need = 1;
+        const uint32_t words = (cb1 - cb0) * 8;
+        for (uint32_t i = tid; i < words; i += GEMV_THREADS) {
+            const uint32_t k = cb0 * 32 + i * 4;
+            int4 v = *(const int4*)(x + k);
+            if (a.prologue == PRO_RMSNORM) {
+                const int4 nw = *(const int4*)(a.norm_w + k);
+                v.x = dn::mul_sat(dn::mul_sat(v.x, scale), nw.x);
+                v.y = dn::mul_sat(dn::mul_sat(v.y, scale), nw.y);
+                v.z = dn::mul_sat(dn::mul_sat(v.z, scale), nw.z);
+                v.w = dn::mul_sat(dn::mul_sat(v.w, scale), nw.w);
+            }
+            const uint64_t d0 = digits5(v.x), d1 = digits5(v.y), d2 = digits5(v.z), d3 = digits5(v.w);
+            need = max(need, max(max(limbs_needed(d0), limbs_needed(d1)), max(limbs_needed(d2), limbs_needed(d3))));
+#pragma unroll
+            for (int l = 0; l < MAX_LIMBS; l++) {
+                const int sh = 8 * l;
+                lds[l * KC_WORDS + i] = (uint32_t)((d0 >> sh) & 0xff) | ((uint32_t)((d1 >> sh) & 0xff) << 8) |
+                                        ((uint32_t)((d2 >> sh) & 0xff) << 16) |
+                                        ((uint32_t)((d3 >> sh) & 0xff) << 24);
+            }
+        }
+        atomicMax(&s_limbs, need);
+        __syncthreads();
+        switch (s_limbs) {
+            case 1: chunk_blocks<1, MODE>(w, tile, cb0, cb1, slot, r, lds, acc64, acc128); break;
+            case 2: chunk_blocks<2, MODE>(w, tile, cb0, cb1, slot, r, lds, acc64, acc128); break;
+            case 3: chunk_blocks<3, MODE>(w, tile, cb0, cb1, slot, r, lds, acc64, acc128); break;
+            case 4: chunk_blocks<4, MODE>(w, tile, cb0, cb1, slot, r, lds, acc64, acc128); break;
+            default: chunk_blocks<5, MODE>(w, tile, cb0, cb1, slot, r, lds, acc64, acc128); break;
+        }
+    }
+
+    dn::i128 total = MODE == Q8_SCALE_ROW ? (dn::i128)acc64 : acc128;
+    total = kgroup_sum(total);
+    if (g == 0) red[wave][r] = total;
+    __syncthreads();
+    if (tid < Q8_TILE_ROWS) {
+        dn::i128 t = 0;
+#pragma unroll
+        for (int i = 0; i < GEMV_WAVES; i++) t += red[i][tid];
+        const uint32_t row = tile * Q8_TILE_ROWS + tid;
+        if (row < w.rows) {
+            if (MODE == Q8_SCALE_ROW) t = t * (dn::i128)w.row_scale[row];
+            int32_t v = dn::round_to_i32(t, 24);
+            if (a.epilogue == EPI_RESIDUAL) v = dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
+            a.out[(size_t)token * a.out_stride + row] = v;
+        }
+    }
+}
+
+// One thread per (row, block): copies the 32 weights into the tile layout
+// and the scale bits into sc16; flags bit 0 = a non-finite scale.
+__global__ void q8_pack_kernel(const uint8_t* raw, uint32_t rows, uint32_t nb, uint8_t* qs, uint16_t* sc16,
+                               int* flags) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * nb) return;
+    const uint32_t row = (uint32_t)(idx / nb), b = (uint32_t)(idx % nb);
+    const uint8_t* src = raw + idx * 34;
+    const uint32_t tile = row / Q8_TILE_ROWS, r = row % Q8_TILE_ROWS;
+    uint8_t* dst = qs + ((size_t)tile * nb + b) * Q8_TILE_BLOCK_BYTES + r * 16;
+#pragma unroll
+    for (int j = 0; j < 16; j++) dst[j] = src[2 + j];
+#pragma unroll
+    for (int j = 0; j < 16; j++) dst[256 + j] = src[18 + j];
+    const uint32_t bits = (uint32_t)src[0] | ((uint32_t)src[1] << 8);
+    sc16[((size_t)tile * nb + b) * Q8_TILE_ROWS + r] = (uint16_t)bits;
+    if (((bits >> 10) & 0x1f) == 0x1f) atomicOr(flags, 1);
+}
+
+// One thread per row: the row's common scale, or flags bit 1 when its blocks
+// differ in value.
+__global__ void q8_row_scale_kernel(const uint16_t* sc16, uint32_t rows, uint32_t nb, int64_t* row_scale,
+                                    int* flags) {
+    const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const uint32_t tile = row / Q8_TILE_ROWS, r = row % Q8_TILE_ROWS;
+    const uint16_t* s = sc16 + (size_t)tile * nb * Q8_TILE_ROWS + r;
+    const int64_t first = dn::scale_q24(s[0]);
+    bool same = true;
+    for (uint32_t b = 1; b < nb; b++) same &= dn::scale_q24(s[(size_t)b * Q8_TILE_ROWS]) == first;
+    row_scale[row] = first;
+    if (!same) atomicOr(flags, 2);
+}
+
+}  // namespace
+
+int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
+    if (a.tokens == 0 || a.w.rows == 0) return 0;
+    if (a.w.cols % 32 || a.x_stride % 4 || ((uintptr_t)a.x & 15)) return IRIS_E_INVALID;
+    if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
+    if (a.tokens > 65535) return IRIS_E_INVALID;
+    dim3 grid(a.w.tiles, a.tokens);
+    switch (a.w.scale_mode) {
+        case Q8_SCALE_ROW: hipLaunchKernelGGL(q8_gemv_kernel<Q8_SCALE_ROW>, grid, dim3(GEMV_THREADS), 0, stream, a); break;
+        case Q8_SCALE_F16: hipLaunchKernelGGL(q8_gemv_kernel<Q8_SCALE_F16>, grid, dim3(GEMV_THREADS), 0, stream, a); break;
+        default: hipLaunchKernelGGL(q8_gemv_kernel<Q8_SCALE_I64>, grid, dim3(GEMV_THREADS), 0, stream, a); break;
+    }
+    return (int)hipGetLastError();
+}
+
+int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream) {
+    int* d_flags = nullptr;
+    int flags = 0;
+    hipError_t st = hipMalloc(&d_flags, sizeof(int));
+    if (st != hipSuccess) return (int)st;
+    st = hipMemsetAsync(d_flags, 0, sizeof(int), stream);
+    const size_t n = (size_t)m->rows * m->nb;
+    if (st == hipSuccess && n) {
+        hipLaunchKernelGGL(q8_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, d_raw, m->rows,
+                           m->nb, m->qs, m->sc16, d_flags);
+        st = hipGetLastError();
+    }
+    if (st == hipSuccess && m->rows) {
+        hipLaunchKernelGGL(q8_row_scale_kernel, dim3((m->rows + 255) / 256), dim3(256), 0, stream, m->sc16, m->rows,
+                           m->nb, m->row_scale, d_flags);
+        st = hipGetLastError();
+    }
+    if (st == hipSuccess) st = hipMemcpyAsync(&flags, d_flags, sizeof(int), hipMemcpyDeviceToHost, stream);
+    if (st == hipSuccess) st = hipStreamSynchronize(stream);
+    hipFree(d_flags);
+    if (st != hipSuccess) return (int)st;
+    if (flags & 1) return IRIS_E_SCALE;
+    m->scale_mode = (flags & 2) ? Q8_SCALE_F16 : Q8_SCALE_ROW;
+    return 0;
+}

@@ -1,0 +1,96 @@
+// Internal declarations shared by the HIP sources of libiris_hip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/iris_hip.h"
+
+// Library-defined error codes (negative, distinct from hipError_t values).
+enum {
+    IRIS_E_INVALID = -1,      // a shape or argument the call does not accept
+    IRIS_E_SCALE = -2,        // a Q8_0 block scale that is not finite
+    IRIS_E_NOMEM = -3,        // host allocation failed
+    IRIS_E_STATE = -4,        // call made in the wrong state (e.g. before finalize)
+    IRIS_E_RANGE = -5,        // position or size past what the object was built for
+};
+
+// Scale layouts of a device Q8_0 matrix.
+enum Q8ScaleMode : int {
+    Q8_SCALE_ROW = 0,  // every block of a row shares one scale: one i64 Q.24 per row
+    Q8_SCALE_F16 = 1,  // one f16 per block (the reference's encoding)
+    Q8_SCALE_I64 = 2,  // one arbitrary i64 Q.24 per block (q8gpu_upload's input)
+};
+
+// Rows per tile and the tiled byte layout:
+//   qs : [tiles][nb][2 halves][16 rows][16 bytes]   (512 B per tile-block)
+//   sc16 / sc64 : [tiles][nb][16 rows]
+//   row_scale : [tiles * 16]
+constexpr int Q8_TILE_ROWS = 16;
+constexpr int Q8_TILE_BLOCK_BYTES = 512;
+
+struct Q8GpuMatrix {
+    uint32_t rows, cols, nb, tiles;
+    int scale_mode;
+    uint8_t* qs;
+    uint16_t* sc16;
+    int64_t* sc64;
+    int64_t* row_scale;
+    uint64_t device_bytes;
+};
+
+// Kernel-side view of a matrix.
+struct Q8View {
+    const uint8_t* qs;
+    const uint16_t* sc16;
+    const int64_t* sc64;
+    const int64_t* row_scale;
+    uint32_t rows, cols, nb, tiles;
+    int scale_mode;
+};
+
+inline Q8View q8_view(const Q8GpuMatrix* m) {
+    return Q8View{m->qs, m->sc16, m->sc64, m->row_scale, m->rows, m->cols, m->nb, m->tiles, m->scale_mode};
+}
+
+// Prologue applied to the activations while they are staged.
+enum GemvPrologue : int {
+    PRO_NONE = 0,
+    PRO_RMSNORM = 1,  // rms_norm(x, norm_w, eps) (ops.rs:98-114), computed per workgroup
+};
+
+// Epilogue applied to each finished output.
+enum GemvEpilogue : int {
+    EPI_STORE = 0,     // out = value
+    EPI_RESIDUAL = 1,  // out = add_sat(value, residual)
+};
+
+struct GemvArgs {
+    Q8View w;
+    const int32_t* x;
+    uint32_t x_stride;
+    uint32_t tokens;
+    int prologue;
+    const int32_t* norm_w;
+    int64_t norm_eps;
+    int epilogue;
+    int32_t* out;
+    uint32_t out_stride;
+    const int32_t* residual;
+    uint32_t residual_stride;
+};
+
+// Launches the exact Q8_0 product out[t][r] = dot_row(x[t], W[r]) (with the
+// prologue/epilogue) on `stream`. Returns a hipError_t value.
+int iris_gemv_launch(const GemvArgs& a, hipStream_t stream);
+
+// Packs raw Q8_0 rows (device memory, reference layout) into m's tiled layout
+// and fills its scales; `m` must have its buffers allocated for `mode`.
+int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream);
+
+// Allocates a matrix from raw Q8_0 bytes in host memory (34-byte blocks).
+int iris_q8_upload_raw(const uint8_t* host_raw, uint32_t rows, uint32_t cols, Q8GpuMatrix** out,
+                       hipStream_t stream);
+
+// Thread-local last-error text for library-defined codes.
+void iris_set_error_text(const char* text);

@@ -1,0 +1,32 @@
+"""The C ABI library loads and exports every function include/iris_hip.h
+declares (no device calls: this runs without a GPU)."""
+import ctypes as C
+import os
+
+import pytest
+
+from iris_amd import native
+
+
+def test_library_is_built():
+    assert os.path.exists(native.LIB_PATH), "run `python -m iris_amd.build` first"
+
+
+def test_every_declared_function_is_exported():
+    names = native.header_functions()
+    assert "q8gpu_product" in names and "q8gpu_upload" in names
+    lib = C.CDLL(native.LIB_PATH)
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_reference_drop_in_symbols_are_present():
+    # The five symbols crates/inference/kernels/src/gpu.rs:45-62 links against.
+    lib = C.CDLL(native.LIB_PATH)
+    for n in ["q8gpu_error", "q8gpu_init", "q8gpu_upload", "q8gpu_free", "q8gpu_product"]:
+        assert hasattr(lib, n)
+
+
+def test_error_text_without_a_device():
+    assert native.error_text(-2) == "Q8_0 block scale is not finite"
+    assert native.error_text(-1)

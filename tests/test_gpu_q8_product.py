@@ -1,0 +1,151 @@
+"""GPU parity of the Q8_0 product against the oracle, through the C ABI.
+
+Cases follow the reference's own device tests
+(crates/inference/kernels/src/gpu.rs:374-495): shapes on and across tiles,
+three magnitude regimes including i32::MIN/MAX activations, exact ties, a
+matrix uploaded through both entry points, and non-finite scales refused.
+Plus the microbenchmark's full sizes.
+"""
+import numpy as np
+import pytest
+
+from iris_amd import native, synth
+from iris_amd.tensor import Q8Matrix, linear_slab_from_source
+from oracle import cpu
+
+pytestmark = pytest.mark.gpu
+
+
+def rand_matrix(rng, rows, cols, max_exponent):
+    """Every weight byte, finite scales of either sign up to max_exponent (gpu.rs:322-334)."""
+    nb = rows * cols // 32
+    v = rng.integers(0, 1 << 62, nb, dtype=np.int64)
+    exponent = (v >> 20) % (max_exponent + 1)
+    bits = ((v & 1) << 15) | (exponent << 10) | ((v >> 4) & 0x3FF)
+    raw = np.empty((nb, 34), np.uint8)
+    raw[:, 0], raw[:, 1] = bits & 0xFF, (bits >> 8) & 0xFF
+    raw[:, 2:] = rng.integers(0, 256, (nb, 32))
+    return raw.reshape(rows, -1)
+
+
+def rand_activations(rng, tokens, cols, magnitude_bits):
+    """i32::MAX / i32::MIN / 0 at 1/61 of positions, else magnitude_bits wide (gpu.rs:336-351)."""
+    r = rng.integers(0, 1 << 62, (tokens, cols), dtype=np.int64)
+    vals = ((r >> 16) & 0xFFFFFFFF).astype(np.uint32).view(np.int32) >> (32 - magnitude_bits)
+    sel = r % 61
+    vals = np.where(sel == 0, np.int32(2 ** 31 - 1), np.where(sel == 1, np.int32(-2 ** 31), np.where(sel == 2, 0, vals)))
+    return vals.astype(np.int32)
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    native.check(native.lib().q8gpu_init(), "q8gpu_init")
+
+
+@pytest.mark.parametrize("rows,cols,tokens", [(1, 32, 1), (16, 32, 16), (17, 64, 15), (130, 96, 33), (300, 1536, 70)])
+@pytest.mark.parametrize("max_exponent,magnitude_bits", [(30, 32), (18, 20), (5, 12)])
+def test_products_equal_one_dot_row_per_value(rows, cols, tokens, max_exponent, magnitude_bits):
+    print(f"shape {rows}x{cols} tokens {tokens} regime {max_exponent}/{magnitude_bits}", flush=True)
+    rng = np.random.default_rng(rows * 7919 + cols * 31 + tokens + max_exponent)
+    raw = rand_matrix(rng, rows, cols, max_exponent)
+    x = rand_activations(rng, tokens, cols, magnitude_bits)
+    m = Q8Matrix.from_bytes(raw, rows, cols)
+    got = linear_slab_from_source(x, m)
+    want = cpu.linear_q8(x, raw)
+    assert np.array_equal(got, want)
+
+
+def test_products_round_ties_to_even():
+    # gpu.rs:397-418: scale 2^-15, activations in steps of 2^-2.
+    rows, cols, tokens = 64, 32, 96
+    raw = np.zeros((rows, 34), np.uint8)
+    raw[:, 0], raw[:, 1] = 0x00, 0x02
+    for row in range(rows):
+        raw[row, 2 + row % 32] = np.uint8(np.int8([1, -1, 3, -3, 5, -7, 127, -128][row % 8]))
+    idx = np.arange(tokens * cols)
+    x = (((idx // cols) - 48 + (idx % cols)) << 14).astype(np.int32).reshape(tokens, cols)
+    got = linear_slab_from_source(x, Q8Matrix.from_bytes(raw, rows, cols))
+    assert np.array_equal(got, cpu.linear_q8(x, raw))
+
+
+def test_reference_upload_entry_point_and_wide_scales():
+    rng = np.random.default_rng(11)
+    rows, cols, tokens = 130, 96, 33
+    raw = rand_matrix(rng, rows, cols, 18)
+    x = rand_activations(rng, tokens, cols, 20)
+    blocks = raw.reshape(-1, 34)
+    weights = blocks[:, 2:].view(np.int8).reshape(rows, cols)
+    bits = blocks[:, 0].astype(np.int64) | (blocks[:, 1].astype(np.int64) << 8)
+    e, mant = (bits >> 10) & 31, bits & 1023
+    q24 = np.where(e == 0, mant, (1024 + mant) << np.maximum(e - 1, 0))
+    q24 = np.where(bits & 0x8000, -q24, q24).reshape(rows, cols // 32)
+    via_f16 = Q8Matrix.from_weights_and_scales(weights, q24)
+    assert via_f16.info()["scale_mode"] == "f16"
+    assert np.array_equal(linear_slab_from_source(x, via_f16), cpu.linear_q8(x, raw))
+    # Scales no f16 can hold stay i64 per block; the product is still exact.
+    wide = q24 * 3 + 1
+    m = Q8Matrix.from_weights_and_scales(weights, wide)
+    assert m.info()["scale_mode"] == "i64"
+    got = linear_slab_from_source(x, m)
+    for t in range(0, tokens, 5):
+        for r in range(0, rows, 7):
+            total = sum(int(np.dot(weights[r, b * 32:(b + 1) * 32].astype(np.int64),
+                                   x[t, b * 32:(b + 1) * 32].astype(np.int64))) * int(wide[r, b])
+                        for b in range(cols // 32))
+            fl, rem = total >> 24, total & ((1 << 24) - 1)
+            want = fl + 1 if rem > (1 << 23) or (rem == (1 << 23) and fl & 1) else fl
+            assert got[t, r] == max(-2 ** 31, min(2 ** 31 - 1, want))
+
+
+def test_uniform_row_scales_take_the_row_path():
+    m = synth.q8_matrix(123, 48, 256, 0x0C00, per_row_scale=True)
+    q = Q8Matrix.from_bytes(m, 48, 256)
+    assert q.info()["scale_mode"] == "row"
+    rng = np.random.default_rng(4)
+    x = rand_activations(rng, 9, 256, 32)
+    assert np.array_equal(linear_slab_from_source(x, q), cpu.linear_q8(x, m))
+
+
+def test_non_finite_scales_are_refused():
+    raw = np.zeros((1, 34), np.uint8)
+    raw[0, 1] = 0x7C
+    with pytest.raises(native.IrisError) as e:
+        Q8Matrix.from_bytes(raw, 1, 32)
+    assert e.value.code == -2
+
+
+def test_no_tokens_and_width_mismatch():
+    m = Q8Matrix.from_bytes(np.zeros((4, 34), np.uint8), 4, 32)
+    assert linear_slab_from_source(np.zeros((0, 32), np.int32), m).shape == (0, 4)
+    with pytest.raises(ValueError):
+        linear_slab_from_source(np.zeros((2, 64), np.int32), m)
+
+
+@pytest.mark.parametrize("per_row_scale", [True, False])
+def test_microbench_gemv_full_size(per_row_scale):
+    # BASELINE configuration 2, GEMV case: M=1, K=4096, N=14336, every output.
+    N, K = 14336, 4096
+    raw = synth.q8_matrix(synth.tensor_seed(2, 1), N, K, synth.scale_base_for(K), per_row_scale)
+    rng = np.random.default_rng(2)
+    s_t = 256 + int(rng.integers(0, 256))
+    x = (rng.integers(-127, 128, (1, K)) * s_t).astype(np.int32)
+    m = Q8Matrix.from_bytes(raw, N, K)
+    assert m.info()["scale_mode"] == ("row" if per_row_scale else "f16")
+    assert np.array_equal(linear_slab_from_source(x, m), cpu.linear_q8(x, raw))
+
+
+def test_microbench_gemm_full_size_sampled_rows():
+    # BASELINE configuration 2, GEMM case: M=512, K=N=4096; every token of
+    # 96 sampled rows against the oracle, plus the stress (full-range) set.
+    N, K, M = 4096, 4096, 512
+    raw = synth.q8_matrix(synth.tensor_seed(2, 2), N, K, synth.scale_base_for(K), True)
+    rng = np.random.default_rng(3)
+    s = (256 + rng.integers(0, 256, (M, 1))).astype(np.int64)
+    x = (rng.integers(-127, 128, (M, K)) * s).astype(np.int32)
+    m = Q8Matrix.from_bytes(raw, N, K)
+    got = linear_slab_from_source(x, m)
+    rows = rng.choice(N, 96, replace=False)
+    assert np.array_equal(got[:, rows], cpu.linear_q8(x, raw[rows]))
+    xs = rand_activations(rng, 64, K, 32)
+    got = linear_slab_from_source(xs, m)
+    assert np.array_equal(got[:, rows], cpu.linear_q8(xs, raw[rows]))
