@@ -92,6 +92,94 @@ int iris_memcpy_d2h(void* dst, const void* src, uint64_t bytes);
 int iris_time_product(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens, int32_t* d_out,
                       uint32_t iterations, double* ms_per_product);
 
+/* ------------------------------------------------------------------------
+ * The deterministic token loop, device-resident.
+ *
+ * A model holds one family's weights on the device; a session holds a KV
+ * cache and runs passes over it. Together they replace the reference's
+ * direct-infer executor (crates/inference/direct/src/executor.rs:41-290,
+ * run_layers_and_logits :293-360, run_mistral_layers_and_logits :364-401)
+ * and its per-layer kernels (crates/inference/kernels/src/mistral/layer.rs:107-318,
+ * crates/inference/kernels/src/prefill_range.rs:307-958), with every layer
+ * product going through the same exact Q8_0 arithmetic as
+ * linear_slab_from_source (tensor.rs:437-520).
+ * ---------------------------------------------------------------------- */
+
+typedef struct IrisModel IrisModel;
+typedef struct IrisSession IrisSession;
+
+enum { IRIS_FAMILY_MISTRAL_DENSE = 0, IRIS_FAMILY_GEMMA_DENSE = 1 };
+
+/* Shape scalars, as inference_artifacts::{MistralShape, DirectInferShape}
+ * carry them (crates/inference/artifacts/src/direct.rs:241-290). Fields a
+ * family does not use are ignored. */
+typedef struct IrisModelDesc {
+    int32_t family;
+    uint32_t hidden, layers, heads, kv_heads, head_dim, ffn, vocab;
+    int64_t norm_eps;               /* Q32.32 */
+    uint32_t attention_scale_q32;   /* mistral-dense */
+    uint32_t max_positions;         /* mistral-dense: positions from here on are refused */
+    int32_t tied_head;              /* head reads the embedding table */
+    /* gemma-dense */
+    uint32_t global_head_dim, ple_width, sliding_window, num_kv_shared_layers;
+    int64_t rope_base_sliding, rope_base_full;   /* Q32.32 */
+    int32_t partial_rotary_q16;
+    int32_t embedding_scale, ple_embedding_scale, ple_projection_scalar, ple_input_scale;
+    int32_t final_logit_softcap;
+    const uint8_t* layer_is_sliding;  /* layers entries, 1 = sliding_attention */
+} IrisModelDesc;
+
+int iris_model_create(const IrisModelDesc* desc, IrisModel** out);
+
+/* Hands one tensor to the model under its DETWGT name
+ * (crates/inference/direct/src/model.rs:489-588 naming): width 8 = Q8_0 rows
+ * (rows x cols/32*34 bytes), 32 = int32 Q16.16 values (rows x cols), 64 =
+ * int64 values (the mistral rotation table "rope_inverse_frequencies").
+ * Matrices go to the device as soon as the set they belong to is complete. */
+int iris_model_set_tensor(IrisModel* model, const char* name, int32_t width, const void* data, uint64_t rows,
+                          uint64_t cols);
+
+/* Checks every tensor arrived and finishes the upload. */
+int iris_model_finalize(IrisModel* model);
+void iris_model_free(IrisModel* model);
+/* Device bytes held by the model's weights. */
+uint64_t iris_model_device_bytes(const IrisModel* model);
+
+/* A KV cache for positions 0..max_positions and work space for passes of up
+ * to max_rows rows. */
+int iris_session_create(IrisModel* model, uint32_t max_positions, uint32_t max_rows, IrisSession** out);
+void iris_session_free(IrisSession* session);
+
+/* Greedy generation (executor.rs:143-185): one pass over the prompt rows at
+ * position 0, then per token: select the first maximum, stop at an EOS id or
+ * the budget, else one pass over the selected token's row. out_tokens gets up
+ * to `tokens` ids and *out_count how many were produced; out_logits (nullable,
+ * tokens x vocab) the logits each selection was made from. use_graph = 1
+ * replays each decode pass as a captured HIP graph. */
+int iris_session_generate(IrisSession* session, const int32_t* prompt, uint32_t prompt_len, uint32_t tokens,
+                          const int32_t* eos_ids, uint32_t n_eos, int32_t* out_tokens, uint32_t* out_count,
+                          int32_t* out_logits, int32_t use_graph);
+
+/* The teacher-forced per-layer pass (the chain's layer stages,
+ * crates/inference/staged/src/routines/layer_mistral.rs:80-99 ->
+ * crates/inference/kernels/src/mistral/stage.rs:172-226): every layer over
+ * all `count` rows at position 0, each layer's output rows written to
+ * out_rows (nullable; layers x count x hidden) and hashed into out_hashes
+ * (nullable; layers x 32 bytes, SHA-256 of the layer's output rows as
+ * little-endian int32). */
+int iris_session_layer_pass(IrisSession* session, const int32_t* ids, uint32_t count, int32_t* out_rows,
+                            uint8_t* out_hashes);
+
+/* Times `steps` decode passes (graph replays) after the prompt pass and
+ * reports milliseconds per decode token from HIP events on the session's
+ * stream; the generated ids are written to out_tokens (nullable). */
+int iris_session_time_decode(IrisSession* session, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,
+                             double* ms_per_token, double* prefill_ms, int32_t* out_tokens);
+
+/* SHA-256 (FIPS 180-4) of `len` bytes into out[32]; the hash
+ * iris_session_layer_pass uses. Host code only. */
+int iris_sha256_bytes(const uint8_t* data, uint64_t len, uint8_t* out);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,13 +57,18 @@ int f16_bits_of_q24(int64_t s) {
 
 void iris_set_error_text(const char* text) { g_error_text = text; }
 
-int iris_q8_upload_raw(const uint8_t* host_raw, uint32_t rows, uint32_t cols, Q8GpuMatrix** out,
-                       hipStream_t stream) {
+int iris_q8_upload_parts(const uint8_t* const* parts, const uint32_t* part_rows, int nparts, uint32_t cols,
+                         int interleave, Q8GpuMatrix** out, hipStream_t stream) {
     *out = nullptr;
-    if (rows == 0 || cols == 0 || cols % 32) return IRIS_E_INVALID;
+    if (nparts <= 0 || cols == 0 || cols % 32) return IRIS_E_INVALID;
+    uint32_t rows = 0;
+    for (int i = 0; i < nparts; i++) rows += part_rows[i];
+    if (rows == 0) return IRIS_E_INVALID;
+    if (interleave && (nparts != 2 || part_rows[0] != part_rows[1])) return IRIS_E_INVALID;
     Q8GpuMatrix* m = alloc_matrix(rows, cols);
     if (!m) return IRIS_E_NOMEM;
-    const size_t raw_bytes = (size_t)rows * m->nb * 34;
+    const size_t row_bytes = (size_t)m->nb * 34;
+    const size_t raw_bytes = (size_t)rows * row_bytes;
     const size_t qs_bytes = (size_t)m->tiles * m->nb * Q8_TILE_BLOCK_BYTES;
     const size_t sc_bytes = (size_t)m->tiles * m->nb * Q8_TILE_ROWS * sizeof(uint16_t);
     const size_t rs_bytes = (size_t)m->tiles * Q8_TILE_ROWS * sizeof(int64_t);
@@ -76,9 +81,13 @@ int iris_q8_upload_raw(const uint8_t* host_raw, uint32_t rows, uint32_t cols, Q8
     if (st == hipSuccess) st = hipMemsetAsync(m->qs, 0, qs_bytes, stream);
     if (st == hipSuccess) st = hipMemsetAsync(m->sc16, 0, sc_bytes, stream);
     if (st == hipSuccess) st = hipMemsetAsync(m->row_scale, 0, rs_bytes, stream);
-    if (st == hipSuccess) st = hipMemcpyAsync(d_raw, host_raw, raw_bytes, hipMemcpyHostToDevice, stream);
+    size_t off = 0;
+    for (int i = 0; i < nparts && st == hipSuccess; i++) {
+        st = hipMemcpyAsync(d_raw + off, parts[i], (size_t)part_rows[i] * row_bytes, hipMemcpyHostToDevice, stream);
+        off += (size_t)part_rows[i] * row_bytes;
+    }
     int rc = (int)st;
-    if (rc == 0) rc = iris_q8_pack_device(d_raw, m, stream);
+    if (rc == 0) rc = iris_q8_pack_device(d_raw, m, stream, interleave ? part_rows[0] : 0);
     hipFree(d_raw);
     if (rc != 0) {
         if (rc == IRIS_E_SCALE) iris_set_error_text("Q8_0 block scale is not finite");
@@ -96,6 +105,11 @@ int iris_q8_upload_raw(const uint8_t* host_raw, uint32_t rows, uint32_t cols, Q8
     }
     *out = m;
     return 0;
+}
+
+int iris_q8_upload_raw(const uint8_t* host_raw, uint32_t rows, uint32_t cols, Q8GpuMatrix** out,
+                       hipStream_t stream) {
+    return iris_q8_upload_parts(&host_raw, &rows, 1, cols, 0, out, stream);
 }
 
 extern "C" {

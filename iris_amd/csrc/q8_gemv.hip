@@ -172,28 +172,71 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
     total = kgroup_sum(total);
     if (g == 0) red[wave][r] = total;
     __syncthreads();
-    if (tid < Q8_TILE_ROWS) {
+    if (wave != 0) return;
+    // Wave 0 finishes the tile: lanes 0..15 own its rows.
+    const uint32_t row = tile * Q8_TILE_ROWS + lane;
+    int32_t v = 0;
+    if (lane < Q8_TILE_ROWS) {
         dn::i128 t = 0;
 #pragma unroll
-        for (int i = 0; i < GEMV_WAVES; i++) t += red[i][tid];
-        const uint32_t row = tile * Q8_TILE_ROWS + tid;
-        if (row < w.rows) {
-            if (MODE == Q8_SCALE_ROW) t = t * (dn::i128)w.row_scale[row];
-            int32_t v = dn::round_to_i32(t, 24);
-            if (a.epilogue == EPI_RESIDUAL) v = dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
-            a.out[(size_t)token * a.out_stride + row] = v;
+        for (int i = 0; i < GEMV_WAVES; i++) t += red[i][lane];
+        if (MODE == Q8_SCALE_ROW && row < w.rows) t = t * (dn::i128)w.row_scale[row];
+        v = dn::round_to_i32(t, 24);
+    }
+    const int32_t partner = __shfl_xor(v, 1);  // the other row of an even/odd pair
+    if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
+    switch (a.epilogue) {
+        case EPI_RESIDUAL:
+            a.out[(size_t)token * a.out_stride + row] =
+                dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
+            break;
+        case EPI_SOFTCAP:
+            a.out[(size_t)token * a.out_stride + row] = dn::softcap(v, a.softcap);
+            break;
+        case EPI_SWIGLU:
+        case EPI_GEGLU:
+            if ((row & 1) == 0) {
+                const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v) : dn::gelu(v);
+                a.out[(size_t)token * a.out_stride + (row >> 1)] = dn::mul_sat(act, partner);
+            }
+            break;
+        case EPI_ROPE_KV: {
+            const uint32_t pos = (uint32_t)(*a.d_pos) + token;
+            if (row < a.q_rows + a.kv_rows) {
+                if ((row & 1) == 0) {
+                    int32_t x0 = v, x1 = partner;
+                    // mistral.rs:114-126: pair j of each head, position * f_j.
+                    if (pos != 0) dn::rotate_pair_q30(x0, x1, (int64_t)pos * a.inv_freq[(row % a.head_dim) >> 1]);
+                    if (row < a.q_rows) {
+                        a.out[(size_t)token * a.out_stride + row] = x0;
+                        a.out[(size_t)token * a.out_stride + row + 1] = x1;
+                    } else {
+                        int32_t* kr = a.k_cache + (size_t)pos * a.kv_rows + (row - a.q_rows);
+                        kr[0] = x0;
+                        kr[1] = x1;
+                    }
+                }
+            } else {
+                a.v_cache[(size_t)pos * a.kv_rows + (row - a.q_rows - a.kv_rows)] = v;
+            }
+            break;
         }
+        default:
+            a.out[(size_t)token * a.out_stride + row] = v;
     }
 }
 
 // One thread per (row, block): copies the 32 weights into the tile layout
 // and the scale bits into sc16; flags bit 0 = a non-finite scale.
+// With interleave_half = h > 0, device row 2i reads source row i and row
+// 2i+1 source row h + i.
 __global__ void q8_pack_kernel(const uint8_t* raw, uint32_t rows, uint32_t nb, uint8_t* qs, uint16_t* sc16,
-                               int* flags) {
+                               int* flags, uint32_t interleave_half) {
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (size_t)rows * nb) return;
     const uint32_t row = (uint32_t)(idx / nb), b = (uint32_t)(idx % nb);
-    const uint8_t* src = raw + idx * 34;
+    const uint32_t src_row = interleave_half ? ((row & 1) ? interleave_half + (row >> 1) : (row >> 1)) : row;
+    const uint8_t* src = raw + ((size_t)src_row * nb + b) * 34;
     const uint32_t tile = row / Q8_TILE_ROWS, r = row % Q8_TILE_ROWS;
     uint8_t* dst = qs + ((size_t)tile * nb + b) * Q8_TILE_BLOCK_BYTES + r * 16;
 #pragma unroll
@@ -236,7 +279,7 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
-int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream) {
+int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream, uint32_t interleave_half) {
     int* d_flags = nullptr;
     int flags = 0;
     hipError_t st = hipMalloc(&d_flags, sizeof(int));
@@ -245,7 +288,7 @@ int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream
     const size_t n = (size_t)m->rows * m->nb;
     if (st == hipSuccess && n) {
         hipLaunchKernelGGL(q8_pack_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, d_raw, m->rows,
-                           m->nb, m->qs, m->sc16, d_flags);
+                           m->nb, m->qs, m->sc16, d_flags, interleave_half);
         st = hipGetLastError();
     }
     if (st == hipSuccess && m->rows) {

@@ -63,6 +63,11 @@ enum GemvPrologue : int {
 enum GemvEpilogue : int {
     EPI_STORE = 0,     // out = value
     EPI_RESIDUAL = 1,  // out = add_sat(value, residual)
+    EPI_SOFTCAP = 2,   // out = softcap(value, cap) (cap <= 0 passes through)
+    EPI_SWIGLU = 3,    // rows interleave gate/up: out[row/2] = mul(silu(gate), up)
+    EPI_GEGLU = 4,     // rows interleave gate/up: out[row/2] = mul(gelu(gate), up)
+    EPI_ROPE_KV = 5,   // rows q|k|v: rotate q and k pairs at the token's position
+                       // (mistral consecutive pairs), q -> out, k/v -> caches
 };
 
 struct GemvArgs {
@@ -78,6 +83,13 @@ struct GemvArgs {
     uint32_t out_stride;
     const int32_t* residual;
     uint32_t residual_stride;
+    int32_t softcap;
+    // EPI_ROPE_KV
+    const int32_t* d_pos;       // absolute position of token 0 of this launch
+    const int64_t* inv_freq;    // head_dim/2 Q32.32 angles per position
+    uint32_t head_dim, q_rows, kv_rows;
+    int32_t* k_cache;           // [position][kv_rows]
+    int32_t* v_cache;
 };
 
 // Launches the exact Q8_0 product out[t][r] = dot_row(x[t], W[r]) (with the
@@ -86,11 +98,17 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream);
 
 // Packs raw Q8_0 rows (device memory, reference layout) into m's tiled layout
 // and fills its scales; `m` must have its buffers allocated for `mode`.
-int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream);
+int iris_q8_pack_device(const uint8_t* d_raw, Q8GpuMatrix* m, hipStream_t stream, uint32_t interleave_half = 0);
 
 // Allocates a matrix from raw Q8_0 bytes in host memory (34-byte blocks).
 int iris_q8_upload_raw(const uint8_t* host_raw, uint32_t rows, uint32_t cols, Q8GpuMatrix** out,
                        hipStream_t stream);
+
+// Allocates one matrix from several row-blocks of raw Q8_0 bytes, stacked in
+// order; with `interleave` (two parts of equal rows) device row 2i is part
+// 0's row i and row 2i+1 part 1's row i.
+int iris_q8_upload_parts(const uint8_t* const* parts, const uint32_t* part_rows, int nparts, uint32_t cols,
+                         int interleave, Q8GpuMatrix** out, hipStream_t stream);
 
 // Thread-local last-error text for library-defined codes.
 void iris_set_error_text(const char* text);

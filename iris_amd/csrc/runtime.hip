@@ -1,0 +1,575 @@
+// The device-resident token loop: model upload, sessions with a KV cache,
+// greedy generation and the teacher-forced per-layer pass.
+//
+// A mistral-dense layer (crates/inference/kernels/src/mistral/layer.rs:107-270)
+// runs as five launches:
+//   1. q|k|v product, rms_norm(norm_attention) fused in front, RoPE and the
+//      K/V cache store fused behind;
+//   2. attention over the cache;
+//   3. W_o product + residual;
+//   4. gate/up product (rows interleaved at upload), rms_norm(norm_feed_forward)
+//      in front, mul(silu(gate), up) behind;
+//   5. W_down product + residual.
+// The head is the final-norm product (softcap behind for gemma), and one
+// kernel selects the first maximum and embeds the next row. Positions and
+// the step counter live in device memory, so a decode pass is the same
+// launch sequence every time and is captured once as a HIP graph.
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+#include "layer_kernels.h"
+#include "q8_internal.h"
+#include "runtime_internal.h"
+
+namespace {
+
+constexpr const char* PREFIX = "model.language_model.";
+
+bool starts_with(const std::string& s, const std::string& p) { return s.compare(0, p.size(), p) == 0; }
+
+int layer_of(const std::string& name, std::string* suffix) {
+    const std::string lp = std::string(PREFIX) + "layers.";
+    if (!starts_with(name, lp)) return -1;
+    size_t dot = name.find('.', lp.size());
+    if (dot == std::string::npos) return -1;
+    int layer = std::atoi(name.substr(lp.size(), dot - lp.size()).c_str());
+    *suffix = name.substr(dot + 1);
+    return layer;
+}
+
+#define RT_CHECK(expr)                  \
+    do {                                \
+        int rc_ = (int)(expr);          \
+        if (rc_ != 0) return rc_;       \
+    } while (0)
+
+template <class T>
+hipError_t dev_alloc_copy(T** dst, const void* src, size_t bytes) {
+    hipError_t st = hipMalloc((void**)dst, bytes ? bytes : 4);
+    if (st == hipSuccess && bytes) st = hipMemcpy(*dst, src, bytes, hipMemcpyHostToDevice);
+    return st;
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------- model
+
+int iris_model_build_layer_if_complete(IrisModel* m, uint32_t l) {
+    LayerWeights& L = m->layers[l];
+    auto& p = m->pending[l];
+    const uint32_t H = m->d.hidden;
+    auto have = [&](const char* k) { return p.count(k) != 0; };
+    if (!L.wqkv && have("self_attn.q_proj.weight") && have("self_attn.k_proj.weight") &&
+        have("self_attn.v_proj.weight")) {
+        const HostTensor& q = p["self_attn.q_proj.weight"];
+        const HostTensor& k = p["self_attn.k_proj.weight"];
+        const HostTensor& v = p["self_attn.v_proj.weight"];
+        if (q.cols != H || k.cols != H || v.cols != H || k.rows != v.rows) return IRIS_E_INVALID;
+        const uint8_t* parts[3] = {q.bytes.data(), k.bytes.data(), v.bytes.data()};
+        uint32_t rows[3] = {(uint32_t)q.rows, (uint32_t)k.rows, (uint32_t)v.rows};
+        RT_CHECK(iris_q8_upload_parts(parts, rows, 3, H, 0, &L.wqkv, m->stream));
+        L.q_rows = rows[0];
+        L.kv_rows = rows[1];
+        p.erase("self_attn.q_proj.weight");
+        p.erase("self_attn.k_proj.weight");
+        p.erase("self_attn.v_proj.weight");
+    }
+    if (!L.wgu && have("mlp.gate_proj.weight") && have("mlp.up_proj.weight")) {
+        const HostTensor& g = p["mlp.gate_proj.weight"];
+        const HostTensor& u = p["mlp.up_proj.weight"];
+        if (g.cols != H || u.cols != H || g.rows != u.rows) return IRIS_E_INVALID;
+        const uint8_t* parts[2] = {g.bytes.data(), u.bytes.data()};
+        uint32_t rows[2] = {(uint32_t)g.rows, (uint32_t)u.rows};
+        RT_CHECK(iris_q8_upload_parts(parts, rows, 2, H, 1, &L.wgu, m->stream));
+        L.ffn = rows[0];
+        p.erase("mlp.gate_proj.weight");
+        p.erase("mlp.up_proj.weight");
+    }
+    for (auto name : {"self_attn.o_proj.weight", "mlp.down_proj.weight"}) {
+        if (!have(name)) continue;
+        const HostTensor& t = p[name];
+        Q8GpuMatrix** dst = std::strcmp(name, "self_attn.o_proj.weight") == 0 ? &L.wo : &L.wdown;
+        const uint8_t* part = t.bytes.data();
+        uint32_t rows = (uint32_t)t.rows;
+        RT_CHECK(iris_q8_upload_parts(&part, &rows, 1, (uint32_t)t.cols, 0, dst, m->stream));
+        p.erase(name);
+    }
+    return (int)hipStreamSynchronize(m->stream);
+}
+
+extern "C" {
+
+int iris_model_create(const IrisModelDesc* desc, IrisModel** out) {
+    if (!desc || !out) return IRIS_E_INVALID;
+    *out = nullptr;
+    const IrisModelDesc& d = *desc;
+    if (d.family != IRIS_FAMILY_MISTRAL_DENSE) return IRIS_E_INVALID;
+    if (!d.hidden || !d.layers || !d.heads || !d.kv_heads || !d.head_dim || !d.ffn || !d.vocab) return IRIS_E_INVALID;
+    if (d.heads % d.kv_heads || d.head_dim % 4 || d.hidden % 32 || d.norm_eps < 0) return IRIS_E_INVALID;
+    IrisModel* m = new (std::nothrow) IrisModel();
+    if (!m) return IRIS_E_NOMEM;
+    m->d = d;
+    m->layer_is_sliding.assign(d.layers, 0);
+    if (d.layer_is_sliding) m->layer_is_sliding.assign(d.layer_is_sliding, d.layer_is_sliding + d.layers);
+    m->d.layer_is_sliding = nullptr;
+    m->layers.resize(d.layers);
+    m->pending.resize(d.layers);
+    hipError_t st = hipStreamCreate(&m->stream);
+    if (st != hipSuccess) {
+        delete m;
+        return (int)st;
+    }
+    *out = m;
+    return 0;
+}
+
+int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const void* data, uint64_t rows,
+                          uint64_t cols) {
+    if (!m || !cname || !data || m->finalized) return m && m->finalized ? IRIS_E_STATE : IRIS_E_INVALID;
+    const std::string name(cname);
+    size_t bytes;
+    if (width == 8) {
+        if (cols == 0 || cols % 32) return IRIS_E_INVALID;
+        bytes = rows * (cols / 32) * 34;
+    } else if (width == 32) {
+        bytes = rows * cols * 4;
+    } else if (width == 64) {
+        bytes = rows * cols * 8;
+    } else {
+        return IRIS_E_INVALID;
+    }
+    std::string suffix;
+    const int layer = layer_of(name, &suffix);
+    const IrisModelDesc& d = m->d;
+    if (layer >= 0) {
+        if ((uint32_t)layer >= d.layers) return IRIS_E_INVALID;
+        LayerWeights& L = m->layers[layer];
+        if (width == 32 && (suffix == "input_layernorm.weight" || suffix == "pre_feedforward_layernorm.weight")) {
+            if (rows * cols != d.hidden) return IRIS_E_INVALID;
+            int32_t** dst = suffix == "input_layernorm.weight" ? &L.norm_attn : &L.norm_ff;
+            RT_CHECK(dev_alloc_copy(dst, data, bytes));
+            return 0;
+        }
+        if (width != 8) return 0;  // tensors the family does not read are ignored
+        HostTensor t;
+        t.rows = rows;
+        t.cols = cols;
+        try {
+            t.bytes.assign((const uint8_t*)data, (const uint8_t*)data + bytes);
+        } catch (...) {
+            return IRIS_E_NOMEM;
+        }
+        m->pending[layer][suffix] = std::move(t);
+        return iris_model_build_layer_if_complete(m, (uint32_t)layer);
+    }
+    if (name == std::string(PREFIX) + "embed_tokens.weight") {
+        if (width != 8 || rows != d.vocab || cols != d.hidden) return IRIS_E_INVALID;
+        RT_CHECK(dev_alloc_copy(&m->embed_raw, data, bytes));
+        m->embed_row_bytes = (uint32_t)(cols / 32 * 34);
+        if (d.tied_head) {
+            const uint8_t* part = (const uint8_t*)data;
+            uint32_t r = (uint32_t)rows;
+            RT_CHECK(iris_q8_upload_parts(&part, &r, 1, (uint32_t)cols, 0, &m->head, m->stream));
+        }
+        return (int)hipStreamSynchronize(m->stream);
+    }
+    if (name == std::string(PREFIX) + "lm_head.weight") {
+        if (d.tied_head) return 0;
+        if (width != 8 || rows != d.vocab || cols != d.hidden) return IRIS_E_INVALID;
+        const uint8_t* part = (const uint8_t*)data;
+        uint32_t r = (uint32_t)rows;
+        RT_CHECK(iris_q8_upload_parts(&part, &r, 1, (uint32_t)cols, 0, &m->head, m->stream));
+        return (int)hipStreamSynchronize(m->stream);
+    }
+    if (name == std::string(PREFIX) + "norm.weight") {
+        if (width != 32 || rows * cols != d.hidden) return IRIS_E_INVALID;
+        RT_CHECK(dev_alloc_copy(&m->final_norm, data, bytes));
+        return 0;
+    }
+    if (name == "rope_inverse_frequencies") {
+        if (width != 64 || rows * cols != d.head_dim / 2) return IRIS_E_INVALID;
+        const int64_t* f = (const int64_t*)data;
+        for (uint64_t i = 0; i < rows * cols; i++)
+            if (f[i] < 0 || f[i] > ((int64_t)1 << 32)) return IRIS_E_INVALID;  // layer.rs:75-83
+        RT_CHECK(dev_alloc_copy(&m->inv_freq, data, bytes));
+        return 0;
+    }
+    return 0;
+}
+
+int iris_model_finalize(IrisModel* m) {
+    if (!m) return IRIS_E_INVALID;
+    const IrisModelDesc& d = m->d;
+    if (!m->embed_raw || !m->head || !m->final_norm || !m->inv_freq) return IRIS_E_STATE;
+    for (uint32_t l = 0; l < d.layers; l++) {
+        const LayerWeights& L = m->layers[l];
+        if (!L.wqkv || !L.wo || !L.wgu || !L.wdown || !L.norm_attn || !L.norm_ff) return IRIS_E_STATE;
+        if (L.q_rows != d.heads * d.head_dim || L.kv_rows != d.kv_heads * d.head_dim || L.ffn != d.ffn)
+            return IRIS_E_INVALID;
+        if (L.wo->rows != d.hidden || L.wo->cols != L.q_rows || L.wdown->rows != d.hidden || L.wdown->cols != d.ffn)
+            return IRIS_E_INVALID;
+        m->pending[l].clear();
+    }
+    m->finalized = true;
+    return 0;
+}
+
+uint64_t iris_model_device_bytes(const IrisModel* m) {
+    if (!m) return 0;
+    uint64_t b = 0;
+    for (const auto& L : m->layers)
+        for (const Q8GpuMatrix* w : {L.wqkv, L.wo, L.wgu, L.wdown})
+            if (w) b += w->device_bytes;
+    if (m->head) b += m->head->device_bytes;
+    return b;
+}
+
+void iris_model_free(IrisModel* m) {
+    if (!m) return;
+    for (auto& L : m->layers) {
+        q8gpu_free(L.wqkv);
+        q8gpu_free(L.wo);
+        q8gpu_free(L.wgu);
+        q8gpu_free(L.wdown);
+        hipFree(L.norm_attn);
+        hipFree(L.norm_ff);
+    }
+    q8gpu_free(m->head);
+    hipFree(m->embed_raw);
+    hipFree(m->final_norm);
+    hipFree(m->inv_freq);
+    if (m->stream) hipStreamDestroy(m->stream);
+    delete m;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------- session
+
+static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    const uint32_t H = d.hidden;
+    const uint32_t qw = d.heads * d.head_dim, kvw = d.kv_heads * d.head_dim;
+    hipStream_t st = s->stream;
+    for (uint32_t l = 0; l < d.layers; l++) {
+        const LayerWeights& L = m->layers[l];
+        GemvArgs g{};
+        // 1. q|k|v = W_qkv rms_norm(x); RoPE; K/V into the cache.
+        g.w = q8_view(L.wqkv);
+        g.x = s->x;
+        g.x_stride = H;
+        g.tokens = rows;
+        g.prologue = PRO_RMSNORM;
+        g.norm_w = L.norm_attn;
+        g.norm_eps = d.norm_eps;
+        g.epilogue = EPI_ROPE_KV;
+        g.out = s->q;
+        g.out_stride = qw;
+        g.d_pos = s->d_pos;
+        g.inv_freq = m->inv_freq;
+        g.head_dim = d.head_dim;
+        g.q_rows = qw;
+        g.kv_rows = kvw;
+        g.k_cache = s->k_cache[l];
+        g.v_cache = s->v_cache[l];
+        RT_CHECK(iris_gemv_launch(g, st));
+        // 2. attention.
+        AttnArgs a{};
+        a.q = s->q;
+        a.q_stride = qw;
+        a.k_cache = s->k_cache[l];
+        a.v_cache = s->v_cache[l];
+        a.kv_stride = kvw;
+        a.ctx = s->ctx;
+        a.ctx_stride = qw;
+        a.d_pos = s->d_pos;
+        a.heads = d.heads;
+        a.kv_heads = d.kv_heads;
+        a.head_dim = d.head_dim;
+        a.scaled = 1;
+        a.scale_q32 = d.attention_scale_q32;
+        a.window = 0;
+        RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
+        // 3. attended = W_o ctx + x.
+        g = GemvArgs{};
+        g.w = q8_view(L.wo);
+        g.x = s->ctx;
+        g.x_stride = qw;
+        g.tokens = rows;
+        g.epilogue = EPI_RESIDUAL;
+        g.out = s->attended;
+        g.out_stride = H;
+        g.residual = s->x;
+        g.residual_stride = H;
+        RT_CHECK(iris_gemv_launch(g, st));
+        // 4. gated = mul(silu(W_gate m), W_up m), m = rms_norm(attended).
+        g = GemvArgs{};
+        g.w = q8_view(L.wgu);
+        g.x = s->attended;
+        g.x_stride = H;
+        g.tokens = rows;
+        g.prologue = PRO_RMSNORM;
+        g.norm_w = L.norm_ff;
+        g.norm_eps = d.norm_eps;
+        g.epilogue = EPI_SWIGLU;
+        g.out = s->gated;
+        g.out_stride = d.ffn;
+        RT_CHECK(iris_gemv_launch(g, st));
+        // 5. x = W_down gated + attended.
+        g = GemvArgs{};
+        g.w = q8_view(L.wdown);
+        g.x = s->gated;
+        g.x_stride = d.ffn;
+        g.tokens = rows;
+        g.epilogue = EPI_RESIDUAL;
+        g.out = s->x;
+        g.out_stride = H;
+        g.residual = s->attended;
+        g.residual_stride = H;
+        RT_CHECK(iris_gemv_launch(g, st));
+        if (layer_rows_out)
+            RT_CHECK(hipMemcpyAsync(layer_rows_out + (size_t)l * rows * H, s->x, (size_t)rows * H * 4,
+                                    hipMemcpyDeviceToHost, st));
+    }
+    return 0;
+}
+
+static int session_head_select(IrisSession* s, uint32_t rows) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    GemvArgs g{};
+    g.w = q8_view(m->head);
+    g.x = s->x + (size_t)(rows - 1) * d.hidden;
+    g.x_stride = d.hidden;
+    g.tokens = 1;
+    g.prologue = PRO_RMSNORM;
+    g.norm_w = m->final_norm;
+    g.norm_eps = d.norm_eps;
+    g.epilogue = EPI_STORE;
+    g.out = s->logits;
+    g.out_stride = d.vocab;
+    RT_CHECK(iris_gemv_launch(g, s->stream));
+    SelectArgs a{};
+    a.logits = s->logits;
+    a.vocab = d.vocab;
+    a.tokens_out = s->tokens;
+    a.logits_keep = s->keep_logits ? s->logits_keep : nullptr;
+    a.d_step = s->d_step;
+    a.d_pos = s->d_pos;
+    a.rows_in_pass = rows;
+    a.embed_raw = m->embed_raw;
+    a.row_bytes = m->embed_row_bytes;
+    a.hidden = d.hidden;
+    a.embed_scale = 0;
+    a.x_next = s->x;
+    return iris_select_embed_launch(a, s->stream);
+}
+
+static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t count) {
+    IrisModel* m = s->model;
+    for (uint32_t i = 0; i < count; i++)
+        if (ids[i] < 0 || (uint32_t)ids[i] >= m->d.vocab) return IRIS_E_INVALID;
+    RT_CHECK(hipMemsetAsync(s->d_pos, 0, sizeof(int32_t), s->stream));
+    RT_CHECK(hipMemsetAsync(s->d_step, 0, sizeof(int32_t), s->stream));
+    RT_CHECK(hipMemcpyAsync(s->ids, ids, (size_t)count * 4, hipMemcpyHostToDevice, s->stream));
+    return iris_embed_rows_launch(s->ids, count, m->embed_raw, m->embed_row_bytes, m->d.hidden, 0, s->x, s->stream);
+}
+
+// Captures the decode pass (one row, head, select) as a graph once.
+static int ensure_graph(IrisSession* s) {
+    if (s->graph_exec && s->graph_keep_logits == s->keep_logits) return 0;
+    if (s->graph_exec) {
+        hipGraphExecDestroy(s->graph_exec);
+        s->graph_exec = nullptr;
+    }
+    hipGraph_t graph = nullptr;
+    RT_CHECK(hipStreamBeginCapture(s->stream, hipStreamCaptureModeThreadLocal));
+    int rc = session_pass(s, 1, nullptr);
+    if (rc == 0) rc = session_head_select(s, 1);
+    hipError_t st = hipStreamEndCapture(s->stream, &graph);
+    if (rc == 0) rc = (int)st;
+    if (rc == 0) rc = (int)hipGraphInstantiate(&s->graph_exec, graph, nullptr, nullptr, 0);
+    if (graph) hipGraphDestroy(graph);
+    if (rc == 0) s->graph_keep_logits = s->keep_logits;
+    return rc;
+}
+
+static int session_decode_pass(IrisSession* s, int use_graph) {
+    if (!use_graph) {
+        RT_CHECK(session_pass(s, 1, nullptr));
+        return session_head_select(s, 1);
+    }
+    RT_CHECK(ensure_graph(s));
+    return (int)hipGraphLaunch(s->graph_exec, s->stream);
+}
+
+extern "C" {
+
+int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows, IrisSession** out) {
+    if (!m || !out || !m->finalized || max_positions == 0 || max_rows == 0) return IRIS_E_INVALID;
+    *out = nullptr;
+    const IrisModelDesc& d = m->d;
+    if (max_rows > max_positions || max_positions > ATTN_MAX_KEYS) return IRIS_E_RANGE;
+    IrisSession* s = new (std::nothrow) IrisSession();
+    if (!s) return IRIS_E_NOMEM;
+    s->model = m;
+    s->max_positions = max_positions;
+    s->max_rows = max_rows;
+    const size_t qw = (size_t)d.heads * d.head_dim, kvw = (size_t)d.kv_heads * d.head_dim;
+    hipError_t st = hipStreamCreate(&s->stream);
+    s->k_cache.assign(d.layers, nullptr);
+    s->v_cache.assign(d.layers, nullptr);
+    for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++) {
+        st = hipMalloc((void**)&s->k_cache[l], (size_t)max_positions * kvw * 4);
+        if (st == hipSuccess) st = hipMalloc((void**)&s->v_cache[l], (size_t)max_positions * kvw * 4);
+    }
+    auto alloc = [&](int32_t** p, size_t n) {
+        if (st == hipSuccess) st = hipMalloc((void**)p, (n ? n : 1) * 4);
+    };
+    alloc(&s->x, (size_t)max_rows * d.hidden);
+    alloc(&s->attended, (size_t)max_rows * d.hidden);
+    alloc(&s->q, (size_t)max_rows * qw);
+    alloc(&s->ctx, (size_t)max_rows * qw);
+    alloc(&s->gated, (size_t)max_rows * d.ffn);
+    alloc(&s->logits, d.vocab);
+    alloc(&s->ids, max_rows);
+    alloc(&s->tokens, max_positions + 1);
+    alloc(&s->d_pos, 1);
+    alloc(&s->d_step, 1);
+    if (st != hipSuccess) {
+        iris_session_free(s);
+        return (int)st;
+    }
+    *out = s;
+    return 0;
+}
+
+void iris_session_free(IrisSession* s) {
+    if (!s) return;
+    if (s->graph_exec) hipGraphExecDestroy(s->graph_exec);
+    for (auto p : s->k_cache) hipFree(p);
+    for (auto p : s->v_cache) hipFree(p);
+    for (int32_t* p : {s->x, s->attended, s->q, s->ctx, s->gated, s->logits, s->ids, s->tokens, s->d_pos, s->d_step,
+                       s->logits_keep})
+        hipFree(p);
+    if (s->stream) hipStreamDestroy(s->stream);
+    delete s;
+}
+
+int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t tokens,
+                          const int32_t* eos_ids, uint32_t n_eos, int32_t* out_tokens, uint32_t* out_count,
+                          int32_t* out_logits, int32_t use_graph) {
+    if (!s || !prompt || !out_tokens || !out_count) return IRIS_E_INVALID;
+    *out_count = 0;
+    if (prompt_len == 0 || tokens == 0) return tokens == 0 ? 0 : IRIS_E_INVALID;
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    if (prompt_len > s->max_rows) return IRIS_E_RANGE;
+    // The last pass runs at position prompt_len + tokens - 2.
+    const uint64_t end = (uint64_t)prompt_len + tokens - 1;
+    if (end > s->max_positions || end > d.max_positions) return IRIS_E_RANGE;
+    s->keep_logits = out_logits != nullptr;
+    if (s->keep_logits) {
+        const size_t need = (size_t)tokens * d.vocab;
+        if (need > s->logits_keep_cap) {
+            hipFree(s->logits_keep);
+            s->logits_keep = nullptr;
+            s->logits_keep_cap = 0;
+            RT_CHECK(hipMalloc((void**)&s->logits_keep, need * 4));
+            s->logits_keep_cap = need;
+        }
+    }
+    RT_CHECK(session_reset_and_embed(s, prompt, prompt_len));
+    RT_CHECK(session_pass(s, prompt_len, nullptr));
+    RT_CHECK(session_head_select(s, prompt_len));
+    for (uint32_t t = 1; t < tokens; t++) RT_CHECK(session_decode_pass(s, use_graph));
+    RT_CHECK(hipMemcpyAsync(out_tokens, s->tokens, (size_t)tokens * 4, hipMemcpyDeviceToHost, s->stream));
+    if (out_logits)
+        RT_CHECK(hipMemcpyAsync(out_logits, s->logits_keep, (size_t)tokens * d.vocab * 4, hipMemcpyDeviceToHost,
+                                s->stream));
+    RT_CHECK(hipStreamSynchronize(s->stream));
+    // Stop at the first EOS (it is kept), as executor.rs:163-168 does; the
+    // passes after it do not change the tokens before it.
+    uint32_t count = tokens;
+    for (uint32_t t = 0; t < tokens; t++) {
+        bool eos = false;
+        for (uint32_t e = 0; e < n_eos; e++) eos |= out_tokens[t] == eos_ids[e];
+        if (eos) {
+            count = t + 1;
+            break;
+        }
+    }
+    *out_count = count;
+    return 0;
+}
+
+int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, int32_t* out_rows,
+                            uint8_t* out_hashes) {
+    if (!s || !ids || count == 0) return IRIS_E_INVALID;
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    if (count > s->max_rows || count > d.max_positions) return IRIS_E_RANGE;
+    std::vector<int32_t> rows;
+    int32_t* dst = out_rows;
+    if (!dst && out_hashes) {
+        try {
+            rows.resize((size_t)d.layers * count * d.hidden);
+        } catch (...) {
+            return IRIS_E_NOMEM;
+        }
+        dst = rows.data();
+    }
+    RT_CHECK(session_reset_and_embed(s, ids, count));
+    RT_CHECK(session_pass(s, count, dst));
+    RT_CHECK(hipStreamSynchronize(s->stream));
+    if (out_hashes)
+        for (uint32_t l = 0; l < d.layers; l++)
+            iris_sha256((const uint8_t*)(dst + (size_t)l * count * d.hidden), (size_t)count * d.hidden * 4,
+                        out_hashes + 32 * l);
+    return 0;
+}
+
+int iris_session_time_decode(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,
+                             double* ms_per_token, double* prefill_ms, int32_t* out_tokens) {
+    if (!s || !prompt || !ms_per_token || steps == 0) return IRIS_E_INVALID;
+    const IrisModelDesc& d = s->model->d;
+    if (prompt_len == 0 || prompt_len > s->max_rows) return IRIS_E_RANGE;
+    const uint64_t end = (uint64_t)prompt_len + steps;
+    if (end > s->max_positions || end > d.max_positions) return IRIS_E_RANGE;
+    s->keep_logits = false;
+    hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
+    RT_CHECK(hipEventCreate(&e0));
+    RT_CHECK(hipEventCreate(&e1));
+    RT_CHECK(hipEventCreate(&e2));
+    int rc = session_reset_and_embed(s, prompt, prompt_len);
+    if (rc == 0) rc = (int)hipEventRecord(e0, s->stream);
+    if (rc == 0) rc = session_pass(s, prompt_len, nullptr);
+    if (rc == 0) rc = session_head_select(s, prompt_len);
+    // Capture (outside the timed region) before timing the replays.
+    if (rc == 0) rc = (int)hipEventRecord(e1, s->stream);
+    if (rc == 0) rc = ensure_graph(s);
+    float pre = 0.f, dec = 0.f;
+    if (rc == 0) rc = (int)hipEventSynchronize(e1);
+    if (rc == 0) rc = (int)hipEventElapsedTime(&pre, e0, e1);
+    if (rc == 0) rc = (int)hipEventRecord(e1, s->stream);
+    for (uint32_t t = 0; rc == 0 && t < steps; t++) rc = (int)hipGraphLaunch(s->graph_exec, s->stream);
+    if (rc == 0) rc = (int)hipEventRecord(e2, s->stream);
+    if (rc == 0) rc = (int)hipEventSynchronize(e2);
+    if (rc == 0) rc = (int)hipEventElapsedTime(&dec, e1, e2);
+    if (rc == 0 && out_tokens)
+        rc = (int)hipMemcpy(out_tokens, s->tokens, (size_t)(steps + 1) * 4, hipMemcpyDeviceToHost);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    hipEventDestroy(e2);
+    if (rc == 0) {
+        *ms_per_token = dec / steps;
+        if (prefill_ms) *prefill_ms = pre;
+    }
+    return rc;
+}
+
+}  // extern "C"

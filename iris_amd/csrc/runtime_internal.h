@@ -1,0 +1,56 @@
+// Model and session state of the device-resident token loop.
+#pragma once
+
+#include <map>
+#include <string>
+#include <vector>
+
+#include "q8_internal.h"
+
+struct HostTensor {
+    uint64_t rows = 0, cols = 0;
+    std::vector<uint8_t> bytes;
+};
+
+struct LayerWeights {
+    Q8GpuMatrix* wqkv = nullptr;   // q|k|v rows stacked
+    Q8GpuMatrix* wo = nullptr;
+    Q8GpuMatrix* wgu = nullptr;    // gate/up rows interleaved
+    Q8GpuMatrix* wdown = nullptr;
+    int32_t* norm_attn = nullptr;
+    int32_t* norm_ff = nullptr;
+    uint32_t q_rows = 0, kv_rows = 0, ffn = 0;
+};
+
+struct IrisModel {
+    IrisModelDesc d{};
+    std::vector<uint8_t> layer_is_sliding;
+    std::vector<LayerWeights> layers;
+    // Q8_0 matrices of a layer waiting for the rest of their set.
+    std::vector<std::map<std::string, HostTensor>> pending;
+    uint8_t* embed_raw = nullptr;   // reference layout, for row lookups
+    uint32_t embed_row_bytes = 0;
+    Q8GpuMatrix* head = nullptr;
+    int32_t* final_norm = nullptr;
+    int64_t* inv_freq = nullptr;
+    hipStream_t stream = nullptr;
+    bool finalized = false;
+};
+
+struct IrisSession {
+    IrisModel* model = nullptr;
+    uint32_t max_positions = 0, max_rows = 0;
+    hipStream_t stream = nullptr;
+    std::vector<int32_t*> k_cache, v_cache;  // per layer [position][kv_heads*head_dim]
+    int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;
+    int32_t *logits = nullptr, *ids = nullptr, *tokens = nullptr;
+    int32_t *d_pos = nullptr, *d_step = nullptr;
+    int32_t* logits_keep = nullptr;
+    size_t logits_keep_cap = 0;
+    bool keep_logits = false;
+    hipGraphExec_t graph_exec = nullptr;
+    bool graph_keep_logits = false;
+};
+
+// SHA-256 (FIPS 180-4) of `len` bytes into out[32].
+void iris_sha256(const uint8_t* data, size_t len, uint8_t out[32]);

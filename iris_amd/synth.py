@@ -7,16 +7,18 @@ Two generators:
   same integer xorshift32 sequence, tensor order and Q8_0 packing, so a
   regenerated ``model.detwgt`` is byte-identical to the checked-in one
   (pinned by its SHA-256).
-* ``counter_hash`` is a counter-based splitmix64, vectorised in numpy and
-  reproduced bit-for-bit by the HIP library's device-side generator, so
-  multi-GB configurations are generated where they are used.
+* ``counter_hash`` is a counter-based splitmix64, vectorised in numpy: any
+  row of any tensor can be generated on its own, so multi-GB configurations
+  are generated on several threads and a checker can regenerate sampled rows.
 
 Config builders cover the workloads this library is measured on: a tiny
 gemma-dense model, Gemma-2B and Mistral-7B shapes, and small test shapes.
 """
 from __future__ import annotations
 
+import concurrent.futures as cf
 import math
+import os
 import struct
 
 import numpy as np
@@ -187,25 +189,42 @@ def counter_hash(tseed: int, start: int, count: int) -> np.ndarray:
         return splitmix64(idx * np.uint64(GOLDEN) ^ np.uint64(tseed))
 
 
-def q8_matrix(tseed: int, rows: int, cols: int, scale_base: int, per_row_scale: bool) -> np.ndarray:
-    """Q8_0 bytes [rows, cols/32*34]: weights (byte % 255) - 127 from one hash
-    per 8 weights; f16 scale bits ``scale_base + h % 64``, one per row
-    (``per_row_scale``, every block of a row repeating it) or one per block.
-    The device generator writes the same bytes."""
-    nb = cols // 32
-    out = np.empty((rows, nb, 34), dtype=np.uint8)
-    h = counter_hash(tseed, 0, rows * nb * 4)
-    q = h.view(np.uint8).reshape(rows, nb, 32)
-    out[:, :, 2:] = ((q.astype(np.int16) % 255) - 127).astype(np.int8).view(np.uint8)
+# (byte % 255) - 127 as an int8 bit pattern, for every byte value.
+_Q_LUT = (((np.arange(256) % 255) - 127).astype(np.int8)).view(np.uint8)
+
+
+def _q8_rows(tseed: int, r0: int, r1: int, nb: int, scale_base: int, per_row_scale: bool, out: np.ndarray):
+    rows = r1 - r0
+    h = counter_hash(tseed, r0 * nb * 4, rows * nb * 4)
+    blk = out[r0:r1].reshape(rows, nb, 34)
+    blk[:, :, 2:] = _Q_LUT[h.view(np.uint8).reshape(rows, nb, 32)]
     salt = tseed ^ 0x5CA1E5CA1E5CA1E5
     if per_row_scale:
-        s = (counter_hash(salt, 0, rows) % np.uint64(64)).astype(np.int64) + scale_base
-        s = np.repeat(s[:, None], nb, axis=1)
+        s = (counter_hash(salt, r0, rows) % np.uint64(64)).astype(np.int64) + scale_base
+        s = np.broadcast_to(s[:, None], (rows, nb))
     else:
-        s = ((counter_hash(salt, 0, rows * nb) % np.uint64(64)).astype(np.int64) + scale_base).reshape(rows, nb)
-    out[:, :, 0] = (s & 0xFF).astype(np.uint8)
-    out[:, :, 1] = (s >> 8).astype(np.uint8)
-    return out.reshape(rows, nb * 34)
+        s = ((counter_hash(salt, r0 * nb, rows * nb) % np.uint64(64)).astype(np.int64) + scale_base).reshape(rows, nb)
+    blk[:, :, 0] = (s & 0xFF).astype(np.uint8)
+    blk[:, :, 1] = (s >> 8).astype(np.uint8)
+
+
+def q8_matrix(tseed: int, rows: int, cols: int, scale_base: int, per_row_scale: bool, threads: int = 0) -> np.ndarray:
+    """Q8_0 bytes [rows, cols/32*34]: weights (byte % 255) - 127 from one hash
+    per 8 weights (hash index (row*nb + block)*4 + j covers bytes 8j..8j+7 of
+    the block); f16 scale bits ``scale_base + h % 64``, one per row
+    (``per_row_scale``, every block of a row repeating it) or one per block.
+    Rows are independent, so large matrices are generated on several threads."""
+    nb = cols // 32
+    out = np.empty((rows, nb * 34), dtype=np.uint8)
+    threads = threads or min(16, os.cpu_count() or 1)
+    chunk = max(1, -(-rows // (threads * 4)))
+    if rows * nb < 65536 or threads == 1:
+        _q8_rows(tseed, 0, rows, nb, scale_base, per_row_scale, out)
+        return out
+    with cf.ThreadPoolExecutor(threads) as ex:
+        list(ex.map(lambda r0: _q8_rows(tseed, r0, min(rows, r0 + chunk), nb, scale_base, per_row_scale, out),
+                    range(0, rows, chunk)))
+    return out
 
 
 def norm_vector(tseed: int, n: int) -> np.ndarray:

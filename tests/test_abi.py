@@ -30,3 +30,12 @@ def test_reference_drop_in_symbols_are_present():
 def test_error_text_without_a_device():
     assert native.error_text(-2) == "Q8_0 block scale is not finite"
     assert native.error_text(-1)
+
+
+def test_layer_hash_is_sha256():
+    # FIPS 180-4 vectors plus lengths around the padding boundary.
+    import hashlib
+    from iris_amd.direct import sha256
+    for data in [b"", b"abc", b"a" * 55, b"a" * 56, b"a" * 64, bytes(range(256)) * 9]:
+        assert sha256(data) == hashlib.sha256(data).hexdigest()
+    assert sha256(b"abc") == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
