@@ -86,11 +86,13 @@ int iris_device_free(void* ptr);
 int iris_memcpy_h2d(void* dst, const void* src, uint64_t bytes);
 int iris_memcpy_d2h(void* dst, const void* src, uint64_t bytes);
 
-/* Runs q8gpu_product_device `iterations` times back to back on one stream
- * after one warm-up call and reports the mean time per product from HIP
- * events recorded on that stream. */
-int iris_time_product(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens, int32_t* d_out,
-                      uint32_t iterations, double* ms_per_product);
+/* Runs q8gpu_product_device `iterations` times back to back on one stream,
+ * cycling through `count` matrices of one shape (so that, with enough of
+ * them, every product reads its weights from HBM rather than from the
+ * last-level cache), after one warm-up pass over all of them, and reports
+ * the mean time per product from HIP events recorded on that stream. */
+int iris_time_product(const Q8GpuMatrix* const* matrices, uint32_t count, const int32_t* d_activations,
+                      uint32_t tokens, int32_t* d_out, uint32_t iterations, double* ms_per_product);
 
 /* ------------------------------------------------------------------------
  * The deterministic token loop, device-resident.

@@ -120,7 +120,11 @@ __device__ __forceinline__ int64_t div_acc_softmax(uint64_t e, uint64_t sum) {
     return (q & 1) == 0 ? (int64_t)q : (int64_t)(q + 1);
 }
 
-// ops.rs:722-771
+// ops.rs:722-771. The reference binary-searches the largest r in
+// [0, i32::MAX] with r*r*x <= 2^64; that r is found here from a double
+// estimate corrected with the same exact u128 test (the test is monotone in
+// r, so the corrected value is the one the search returns), then the same
+// nearest-with-ties-to-even choice between r and r + 1.
 __device__ inline int32_t inv_sqrt_acc(int64_t x) {
     if (x == 0) return INT32_MAX;
     const u128 target = (u128)1 << 64;
@@ -128,12 +132,10 @@ __device__ inline int32_t inv_sqrt_acc(int64_t x) {
     const uint32_t max_bits = (uint32_t)INT32_MAX;
     auto prod = [&](uint32_t c) -> u128 { return (u128)((uint64_t)c * (uint64_t)c) * divisor; };
     if (prod(max_bits) <= target) return INT32_MAX;
-    uint32_t low = 0, high = max_bits;
-    while (low < high) {
-        uint32_t mid = low + ((high - low + 1) >> 1);
-        if (prod(mid) <= target) low = mid;
-        else high = mid - 1;
-    }
+    double est = floor(sqrt(18446744073709551616.0 / (double)(uint64_t)x));
+    uint32_t low = est >= (double)max_bits ? max_bits : (uint32_t)est;
+    while (low < max_bits && prod(low + 1) <= target) low++;
+    while (low > 0 && prod(low) > target) low--;
     uint32_t lower = low;
     uint32_t upper = lower + 1 > max_bits ? max_bits : lower + 1;
     u128 le = target - prod(lower);

@@ -131,6 +131,7 @@ int q8gpu_init(void) {
     void* probe = nullptr;
     hipError_t st = hipMalloc(&probe, 1 << 20);
     if (st != hipSuccess) return (int)st;
+    iris_gemv_prepare();
     return (int)hipFree(probe);
 }
 
@@ -270,23 +271,26 @@ int iris_memcpy_d2h(void* dst, const void* src, uint64_t bytes) {
     return (int)hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
 }
 
-int iris_time_product(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
-                      uint32_t iterations, double* ms_per_product) {
-    if (!m || !ms_per_product || iterations == 0) return IRIS_E_INVALID;
+int iris_time_product(const Q8GpuMatrix* const* ms, uint32_t count, const int32_t* d_act, uint32_t tokens,
+                      int32_t* d_out, uint32_t iterations, double* ms_per_product) {
+    if (!ms || count == 0 || !ms_per_product || iterations == 0) return IRIS_E_INVALID;
+    for (uint32_t i = 0; i < count; i++)
+        if (!ms[i] || ms[i]->rows != ms[0]->rows || ms[i]->cols != ms[0]->cols) return IRIS_E_INVALID;
     hipStream_t s = nullptr;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     hipError_t st = hipStreamCreate(&s);
     if (st == hipSuccess) st = hipEventCreate(&e0);
     if (st == hipSuccess) st = hipEventCreate(&e1);
     int rc = (int)st;
-    if (rc == 0) rc = q8gpu_product_device(m, d_act, tokens, d_out, s);
+    for (uint32_t i = 0; rc == 0 && i < count; i++) rc = q8gpu_product_device(ms[i], d_act, tokens, d_out, s);
     if (rc == 0) rc = (int)hipEventRecord(e0, s);
-    for (uint32_t i = 0; rc == 0 && i < iterations; i++) rc = q8gpu_product_device(m, d_act, tokens, d_out, s);
+    for (uint32_t i = 0; rc == 0 && i < iterations; i++)
+        rc = q8gpu_product_device(ms[i % count], d_act, tokens, d_out, s);
     if (rc == 0) rc = (int)hipEventRecord(e1, s);
     if (rc == 0) rc = (int)hipEventSynchronize(e1);
-    float ms = 0.f;
-    if (rc == 0) rc = (int)hipEventElapsedTime(&ms, e0, e1);
-    if (rc == 0) *ms_per_product = (double)ms / iterations;
+    float elapsed = 0.f;
+    if (rc == 0) rc = (int)hipEventElapsedTime(&elapsed, e0, e1);
+    if (rc == 0) *ms_per_product = (double)elapsed / iterations;
     if (e0) hipEventDestroy(e0);
     if (e1) hipEventDestroy(e1);
     if (s) hipStreamDestroy(s);

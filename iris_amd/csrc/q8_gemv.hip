@@ -48,11 +48,11 @@ __device__ __forceinline__ dn::i128 kgroup_sum(dn::i128 v) {
 }
 
 template <int L>
-__device__ __forceinline__ int64_t block_sum(const uint4 q0, const uint4 q1, const uint32_t* lb) {
+__device__ __forceinline__ int64_t block_sum_pw(const uint4 q0, const uint4 q1, const uint32_t* lb, uint32_t pw) {
     int64_t bs = 0;
 #pragma unroll
     for (int l = 0; l < L; l++) {
-        const uint32_t* p = lb + l * KC_WORDS;
+        const uint32_t* p = lb + l * pw;
         int s = 0;
         s = __builtin_amdgcn_sdot4((int)q0.x, (int)p[0], s, false);
         s = __builtin_amdgcn_sdot4((int)q0.y, (int)p[1], s, false);
@@ -79,7 +79,7 @@ __device__ __forceinline__ void chunk_blocks(const Q8View& w, uint32_t tile, uin
         const uint8_t* qp = qrow + (size_t)b * Q8_TILE_BLOCK_BYTES;
         const uint4 q0 = *(const uint4*)qp;
         const uint4 q1 = *(const uint4*)(qp + 256);
-        const int64_t bs = block_sum<L>(q0, q1, lds + (b - cb0) * 8);
+        const int64_t bs = block_sum_pw<L>(q0, q1, lds + (b - cb0) * 8, KC_WORDS);
         if constexpr (MODE == Q8_SCALE_ROW) {
             acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
         } else if constexpr (MODE == Q8_SCALE_F16) {
@@ -92,6 +92,232 @@ __device__ __forceinline__ void chunk_blocks(const Q8View& w, uint32_t tile, uin
         } else {
             acc128 += (dn::i128)bs * (dn::i128)w.sc64[sbase + (size_t)b * Q8_TILE_ROWS];
         }
+    }
+}
+
+// First maximum of (value, index) pairs: larger value, then smaller index
+// (crates/inference/direct/src/generation.rs:25-33).
+__device__ __forceinline__ void argmax_combine(int32_t& v, uint32_t& i, int32_t ov, uint32_t oi) {
+    if (ov > v || (ov == v && oi < i)) {
+        v = ov;
+        i = oi;
+    }
+}
+
+// The head's epilogue, run by the wave finishing a tile: logits out
+// (softcapped) and the tile's first maximum to the partials; the selection
+// itself is the next kernel's (iris_select_launch).
+__device__ void head_select(const GemvArgs& a, int32_t v, uint32_t row, uint32_t lane, uint32_t tile) {
+    const uint32_t step = (uint32_t)*a.d_step;
+    int32_t best = INT32_MIN;
+    uint32_t best_i = 0xffffffffu;
+    if (lane < Q8_TILE_ROWS && row < a.w.rows) {
+        const int32_t logit = dn::softcap(v, a.softcap);
+        a.out[row] = logit;
+        if (a.logits_keep) a.logits_keep[(size_t)step * a.w.rows + row] = logit;
+        best = logit;
+        best_i = row;
+    }
+    for (int off = 8; off >= 1; off >>= 1) argmax_combine(best, best_i, __shfl_xor(best, off), __shfl_xor(best_i, off));
+    if (lane == 0) a.sel_partial[tile] = ((uint64_t)best_i << 32) | (uint32_t)best;
+}
+
+// Greedy selection (generation.rs:25-57) over the head's tile partials, in
+// tile (= token id) order with the first maximum kept, then the selected
+// token's embedding as the next pass's row (view_kernels.rs:37-57,
+// model.rs:316-330), and the step and position advanced.
+__global__ __launch_bounds__(256) void select_embed_kernel(const GemvArgs a) {
+    __shared__ int32_t s_v[4];
+    __shared__ uint32_t s_i[4];
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    int32_t best = INT32_MIN;
+    uint32_t best_i = 0xffffffffu;
+    for (uint32_t t = tid; t < a.w.tiles; t += 256) {
+        const uint64_t p = a.sel_partial[t];
+        argmax_combine(best, best_i, (int32_t)(uint32_t)p, (uint32_t)(p >> 32));
+    }
+    for (int off = 32; off >= 1; off >>= 1) argmax_combine(best, best_i, __shfl_xor(best, off), __shfl_xor(best_i, off));
+    if (lane == 0) {
+        s_v[wave] = best;
+        s_i[wave] = best_i;
+    }
+    __syncthreads();
+    best = s_v[0];
+    best_i = s_i[0];
+    for (int i = 1; i < 4; i++) argmax_combine(best, best_i, s_v[i], s_i[i]);
+    const uint32_t token = best_i;
+    const uint8_t* er = a.embed_raw + (size_t)token * a.embed_row_bytes;
+    for (uint32_t c = tid; c < a.hidden; c += 256) {
+        const uint8_t* blk = er + (size_t)(c / 32) * 34;
+        const int64_t sc = dn::scale_q24((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        int32_t e = dn::round_to_i32((dn::i128)((int64_t)(int8_t)blk[2 + c % 32] * sc), 8);
+        if (a.embed_scale != 0) e = dn::mul_sat(e, a.embed_scale);
+        a.x_next[c] = e;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        const int32_t step = *a.d_step;
+        a.tokens_out[step] = (int32_t)token;
+        *a.d_step = step + 1;
+        *a.d_pos_rw = *a.d_pos_rw + (int32_t)a.rows_in_pass;
+    }
+}
+
+template <int MODE>
+__device__ void finish_tile(const GemvArgs& a, uint32_t tile, uint32_t token, dn::i128 t, uint32_t lane) {
+    const Q8View& w = a.w;
+    const uint32_t row = tile * Q8_TILE_ROWS + lane;
+    int32_t v = 0;
+    if (lane < Q8_TILE_ROWS) {
+        if (MODE == Q8_SCALE_ROW && row < w.rows) t = t * (dn::i128)w.row_scale[row];
+        v = dn::round_to_i32(t, 24);
+    }
+    const int32_t partner = __shfl_xor(v, 1);  // the other row of an even/odd pair
+    if (a.epilogue == EPI_HEAD_SELECT) {
+        head_select(a, v, row, lane, tile);
+        return;
+    }
+    if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
+    switch (a.epilogue) {
+        case EPI_RESIDUAL:
+            a.out[(size_t)token * a.out_stride + row] =
+                dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
+            break;
+        case EPI_SOFTCAP:
+            a.out[(size_t)token * a.out_stride + row] = dn::softcap(v, a.softcap);
+            break;
+        case EPI_SWIGLU:
+        case EPI_GEGLU:
+            if ((row & 1) == 0) {
+                const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v) : dn::gelu(v);
+                a.out[(size_t)token * a.out_stride + (row >> 1)] = dn::mul_sat(act, partner);
+            }
+            break;
+        case EPI_ROPE_KV: {
+            const uint32_t pos = (uint32_t)(*a.d_pos) + token;
+            if (row < a.q_rows + a.kv_rows) {
+                if ((row & 1) == 0) {
+                    int32_t x0 = v, x1 = partner;
+                    // mistral.rs:114-126: pair j of each head, position * f_j.
+                    if (pos != 0) dn::rotate_pair_q30(x0, x1, (int64_t)pos * a.inv_freq[(row % a.head_dim) >> 1]);
+                    if (row < a.q_rows) {
+                        a.out[(size_t)token * a.out_stride + row] = x0;
+                        a.out[(size_t)token * a.out_stride + row + 1] = x1;
+                    } else {
+                        int32_t* kc = a.k_cache + (size_t)(row - a.q_rows) * a.k_pos_stride + pos;
+                        kc[0] = x0;
+                        kc[a.k_pos_stride] = x1;
+                    }
+                }
+            } else {
+                a.v_cache[(size_t)pos * a.kv_rows + (row - a.q_rows - a.kv_rows)] = v;
+            }
+            break;
+        }
+        default:
+            a.out[(size_t)token * a.out_stride + row] = v;
+    }
+}
+
+// Stages x[4*i0 .. 4*i1) (after the optional rms_norm: mul_sat(mul_sat(v,
+// scale), w)) as MAX_LIMBS digit planes of dwords at planes[l*pw + i - i0];
+// returns the most digits any value needs.
+__device__ __forceinline__ int stage_planes(const int32_t* x, const int32_t* norm_w, int32_t scale, uint32_t i0,
+                                            uint32_t i1, uint32_t* planes, uint32_t pw, uint32_t tid) {
+    int need = 1;
+    for (uint32_t i = i0 + tid; i < i1; i += GEMV_THREADS) {
+        const uint32_t k = i * 4;
+        int4 v = *(const int4*)(x + k);
+        if (norm_w) {
+            const int4 nw = *(const int4*)(norm_w + k);
+            v.x = dn::mul_sat(dn::mul_sat(v.x, scale), nw.x);
+            v.y = dn::mul_sat(dn::mul_sat(v.y, scale), nw.y);
+            v.z = dn::mul_sat(dn::mul_sat(v.z, scale), nw.z);
+            v.w = dn::mul_sat(dn::mul_sat(v.w, scale), nw.w);
+        }
+        const uint64_t d0 = digits5(v.x), d1 = digits5(v.y), d2 = digits5(v.z), d3 = digits5(v.w);
+        need = max(need, max(max(limbs_needed(d0), limbs_needed(d1)), max(limbs_needed(d2), limbs_needed(d3))));
+#pragma unroll
+        for (int l = 0; l < MAX_LIMBS; l++) {
+            const int sh = 8 * l;
+            planes[l * pw + (i - i0)] = (uint32_t)((d0 >> sh) & 0xff) | ((uint32_t)((d1 >> sh) & 0xff) << 8) |
+                                        ((uint32_t)((d2 >> sh) & 0xff) << 16) | ((uint32_t)((d3 >> sh) & 0xff) << 24);
+        }
+    }
+    return need;
+}
+
+// One block's contribution to the lane's accumulator.
+template <int L, int MODE>
+__device__ __forceinline__ void accumulate_block(const uint4 q0, const uint4 q1, uint32_t sbits, int64_t sc64,
+                                                 const uint32_t* lb, uint32_t pw, int64_t& acc64, dn::i128& acc128) {
+    const int64_t bs = block_sum_pw<L>(q0, q1, lb, pw);
+    if constexpr (MODE == Q8_SCALE_ROW) {
+        acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
+    } else if constexpr (MODE == Q8_SCALE_F16) {
+        const uint32_t e = (sbits >> 10) & 0x1f;
+        const int64_t m = (int64_t)(sbits & 0x3ff) | (e ? 1024 : 0);
+        int64_t p = bs * m;  // < 2^55
+        if (sbits & 0x8000) p = -p;
+        acc128 += (dn::i128)p << (e ? e - 1 : 0);
+    } else {
+        acc128 += (dn::i128)bs * (dn::i128)sc64;
+    }
+}
+
+constexpr int BATCH = 2;  // blocks a lane has in flight while it computes the previous batch
+
+// A batch of one lane's blocks: weights and the scale each needs.
+struct BlockBatch {
+    uint4 q[BATCH][2];
+    uint32_t s[BATCH];
+    int64_t w[BATCH];
+};
+
+// Loads blocks slot + (k0 + u) * nslots of a tile; an index past the lane's
+// last block re-reads that block (its result is not used).
+template <int MODE>
+__device__ __forceinline__ void fetch_batch(const Q8View& w, uint32_t tile, uint32_t slot, uint32_t nslots,
+                                            uint32_t last, uint32_t r, uint32_t k0, BlockBatch& bb) {
+    const uint8_t* qrow = w.qs + (size_t)tile * w.nb * Q8_TILE_BLOCK_BYTES + r * 16;
+    const size_t sbase = (size_t)tile * w.nb * Q8_TILE_ROWS + r;
+#pragma unroll
+    for (int u = 0; u < BATCH; u++) {
+        const uint32_t b = min(slot + (k0 + u) * nslots, last);
+        const uint8_t* qp = qrow + (size_t)b * Q8_TILE_BLOCK_BYTES;
+        bb.q[u][0] = *(const uint4*)qp;
+        bb.q[u][1] = *(const uint4*)(qp + 256);
+        if constexpr (MODE == Q8_SCALE_F16) bb.s[u] = w.sc16[sbase + (size_t)b * Q8_TILE_ROWS];
+        if constexpr (MODE == Q8_SCALE_I64) bb.w[u] = w.sc64[sbase + (size_t)b * Q8_TILE_ROWS];
+    }
+}
+
+__device__ __forceinline__ uint32_t lane_block_count(uint32_t nb, uint32_t slot, uint32_t nslots) {
+    return slot < nb ? (nb - slot + nslots - 1) / nslots : 0;
+}
+
+// All of one tile's blocks this lane owns (slot, slot + nslots, ...), against
+// digit planes covering the whole row (plane stride pw dwords). Loads run one
+// batch ahead of the arithmetic.
+template <int L, int MODE>
+__device__ __forceinline__ void tile_blocks(const Q8View& w, uint32_t tile, uint32_t slot, uint32_t nslots, uint32_t r,
+                                            const uint32_t* planes, uint32_t pw, int64_t& acc64, dn::i128& acc128) {
+    const uint32_t cnt = lane_block_count(w.nb, slot, nslots);
+    if (cnt == 0) return;
+    const uint32_t last = slot + (cnt - 1) * nslots;
+    BlockBatch cur, nxt;
+    fetch_batch<MODE>(w, tile, slot, nslots, last, r, 0, cur);
+    for (uint32_t k0 = 0; k0 < cnt; k0 += BATCH) {
+        if (k0 + BATCH < cnt) fetch_batch<MODE>(w, tile, slot, nslots, last, r, k0 + BATCH, nxt);
+#pragma unroll
+        for (int u = 0; u < BATCH; u++) {
+            if (k0 + u < cnt) {
+                const uint32_t b = slot + (k0 + u) * nslots;
+                accumulate_block<L, MODE>(cur.q[u][0], cur.q[u][1], cur.s[u], cur.w[u], planes + b * 8, pw, acc64,
+                                          acc128);
+            }
+        }
+        cur = nxt;
     }
 }
 
@@ -174,55 +400,88 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
     __syncthreads();
     if (wave != 0) return;
     // Wave 0 finishes the tile: lanes 0..15 own its rows.
-    const uint32_t row = tile * Q8_TILE_ROWS + lane;
-    int32_t v = 0;
-    if (lane < Q8_TILE_ROWS) {
-        dn::i128 t = 0;
+    dn::i128 t = 0;
+    if (lane < Q8_TILE_ROWS)
 #pragma unroll
         for (int i = 0; i < GEMV_WAVES; i++) t += red[i][lane];
-        if (MODE == Q8_SCALE_ROW && row < w.rows) t = t * (dn::i128)w.row_scale[row];
-        v = dn::round_to_i32(t, 24);
-    }
-    const int32_t partner = __shfl_xor(v, 1);  // the other row of an even/odd pair
-    if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
-    switch (a.epilogue) {
-        case EPI_RESIDUAL:
-            a.out[(size_t)token * a.out_stride + row] =
-                dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
-            break;
-        case EPI_SOFTCAP:
-            a.out[(size_t)token * a.out_stride + row] = dn::softcap(v, a.softcap);
-            break;
-        case EPI_SWIGLU:
-        case EPI_GEGLU:
-            if ((row & 1) == 0) {
-                const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v) : dn::gelu(v);
-                a.out[(size_t)token * a.out_stride + (row >> 1)] = dn::mul_sat(act, partner);
-            }
-            break;
-        case EPI_ROPE_KV: {
-            const uint32_t pos = (uint32_t)(*a.d_pos) + token;
-            if (row < a.q_rows + a.kv_rows) {
-                if ((row & 1) == 0) {
-                    int32_t x0 = v, x1 = partner;
-                    // mistral.rs:114-126: pair j of each head, position * f_j.
-                    if (pos != 0) dn::rotate_pair_q30(x0, x1, (int64_t)pos * a.inv_freq[(row % a.head_dim) >> 1]);
-                    if (row < a.q_rows) {
-                        a.out[(size_t)token * a.out_stride + row] = x0;
-                        a.out[(size_t)token * a.out_stride + row + 1] = x1;
-                    } else {
-                        int32_t* kr = a.k_cache + (size_t)pos * a.kv_rows + (row - a.q_rows);
-                        kr[0] = x0;
-                        kr[1] = x1;
-                    }
-                }
-            } else {
-                a.v_cache[(size_t)pos * a.kv_rows + (row - a.q_rows - a.kv_rows)] = v;
-            }
-            break;
+    finish_tile<MODE>(a, tile, token, t, lane);
+}
+
+template <int MODE>
+__global__ __launch_bounds__(GEMV_THREADS, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split) {
+    extern __shared__ uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
+    __shared__ dn::i128 red[GEMV_WAVES][Q8_TILE_ROWS];
+    __shared__ int64_t ssq[GEMV_WAVES];
+    __shared__ int32_t s_scale;
+    __shared__ int s_limbs;
+
+    const uint32_t tid = threadIdx.x;
+    const uint32_t wave = tid >> 6, lane = tid & 63;
+    const uint32_t r = lane & 15, g = lane >> 4;
+    const uint32_t token = blockIdx.y;
+    const Q8View& w = a.w;
+    const uint32_t K = w.cols, pw = K / 4;
+    const int32_t* x = a.x + (size_t)token * a.x_stride;
+
+    // Tiles in groups of GEMV_WAVES / split; split waves share a tile's blocks.
+    const uint32_t per_group = GEMV_WAVES / split;
+    const uint32_t groups = (w.tiles + per_group - 1) / per_group;
+    const uint32_t part = wave % split;
+    const uint32_t slot = part * 4 + g, nslots = split * 4;
+
+    // Once per workgroup: the norm scale and every digit plane of the row.
+    int32_t scale = 0;
+    if (a.prologue == PRO_RMSNORM) {
+        int64_t s = 0;
+        for (uint32_t k = tid; k < K; k += GEMV_THREADS) s = dn::acc_add_sat(s, (int64_t)x[k] * x[k]);
+        s = wave_sum_sat_nonneg(s);
+        if (lane == 0) ssq[wave] = s;
+        if (tid == 0) s_limbs = 1;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t t = 0;
+            for (int i = 0; i < GEMV_WAVES; i++) t = dn::acc_add_sat(t, ssq[i]);
+            s_scale = dn::rms_scale_from_sum(t, K, a.norm_eps);
         }
-        default:
-            a.out[(size_t)token * a.out_stride + row] = v;
+        __syncthreads();
+        scale = s_scale;
+    } else {
+        if (tid == 0) s_limbs = 1;
+        __syncthreads();
+    }
+    const int need = stage_planes(x, a.prologue == PRO_RMSNORM ? a.norm_w : nullptr, scale, 0, pw, planes, pw, tid);
+    atomicMax(&s_limbs, need);
+    __syncthreads();
+    const int limbs = s_limbs;
+
+    for (uint32_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+        const uint32_t tile = grp * per_group + wave / split;
+        int64_t acc64 = 0;
+        dn::i128 acc128 = 0;
+        if (tile < w.tiles) {
+            switch (limbs) {
+                case 1: tile_blocks<1, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
+                case 2: tile_blocks<2, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
+                case 3: tile_blocks<3, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
+                case 4: tile_blocks<4, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
+                default: tile_blocks<5, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
+            }
+        }
+        dn::i128 total = MODE == Q8_SCALE_ROW ? (dn::i128)acc64 : acc128;
+        total = kgroup_sum(total);
+        if (split == 1) {
+            if (tile < w.tiles) finish_tile<MODE>(a, tile, token, total, lane);
+            continue;
+        }
+        if (g == 0) red[wave][r] = total;
+        __syncthreads();
+        if (part == 0 && tile < w.tiles) {
+            dn::i128 t = 0;
+            if (lane < Q8_TILE_ROWS)
+                for (uint32_t i = 0; i < split; i++) t += red[wave + i][lane];
+            finish_tile<MODE>(a, tile, token, t, lane);
+        }
+        __syncthreads();
     }
 }
 
@@ -265,11 +524,68 @@ __global__ void q8_row_scale_kernel(const uint16_t* sc16, uint32_t rows, uint32_
 
 }  // namespace
 
+namespace {
+
+constexpr uint32_t PERSISTENT_MAX_K = 24576;  // digit planes of a whole row: 5*K bytes of LDS
+constexpr uint32_t WGS_PER_CU = 2;
+
+int g_num_cus = 0;
+uint32_t g_split_override = 0;
+
+void gemv_prepare_once() {
+    static bool done = false;
+    if (done) return;
+    done = true;
+    int dev = 0;
+    hipDeviceProp_t prop;
+    if (hipGetDevice(&dev) == hipSuccess && hipGetDeviceProperties(&prop, dev) == hipSuccess)
+        g_num_cus = prop.multiProcessorCount;
+    if (g_num_cus <= 0) g_num_cus = 256;
+    const int bytes = MAX_LIMBS * PERSISTENT_MAX_K;
+    hipFuncSetAttribute((const void*)&q8_gemv_persistent<Q8_SCALE_ROW>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    hipFuncSetAttribute((const void*)&q8_gemv_persistent<Q8_SCALE_F16>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    hipFuncSetAttribute((const void*)&q8_gemv_persistent<Q8_SCALE_I64>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
+}
+
+// Waves sharing one tile: enough tile groups for every resident workgroup.
+uint32_t choose_split(uint32_t tiles) {
+    if (g_split_override == 1 || g_split_override == 2 || g_split_override == 4 || g_split_override == 8)
+        return g_split_override;
+    const uint64_t target = (uint64_t)WGS_PER_CU * g_num_cus;
+    for (uint32_t s = 1; s < GEMV_WAVES; s *= 2)
+        if ((uint64_t)tiles * s / GEMV_WAVES >= target) return s;
+    return GEMV_WAVES;
+}
+
+}  // namespace
+
+void iris_gemv_prepare() { gemv_prepare_once(); }
+
+int iris_select_launch(const GemvArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(select_embed_kernel, dim3(1), dim3(256), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
 int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.tokens == 0 || a.w.rows == 0) return 0;
     if (a.w.cols % 32 || a.x_stride % 4 || ((uintptr_t)a.x & 15)) return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
     if (a.tokens > 65535) return IRIS_E_INVALID;
+    gemv_prepare_once();
+    if (a.w.cols <= PERSISTENT_MAX_K) {
+        const uint32_t split = choose_split(a.w.tiles);
+        const uint32_t groups = (a.w.tiles + GEMV_WAVES / split - 1) / (GEMV_WAVES / split);
+        const uint32_t wgs = min(groups, (uint32_t)(WGS_PER_CU * g_num_cus));
+        const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
+        dim3 grid(wgs, a.tokens);
+        switch (a.w.scale_mode) {
+            case Q8_SCALE_ROW: hipLaunchKernelGGL(q8_gemv_persistent<Q8_SCALE_ROW>, grid, dim3(GEMV_THREADS), shmem, stream, a, split); break;
+            case Q8_SCALE_F16: hipLaunchKernelGGL(q8_gemv_persistent<Q8_SCALE_F16>, grid, dim3(GEMV_THREADS), shmem, stream, a, split); break;
+            default: hipLaunchKernelGGL(q8_gemv_persistent<Q8_SCALE_I64>, grid, dim3(GEMV_THREADS), shmem, stream, a, split); break;
+        }
+        return (int)hipGetLastError();
+    }
     dim3 grid(a.w.tiles, a.tokens);
     switch (a.w.scale_mode) {
         case Q8_SCALE_ROW: hipLaunchKernelGGL(q8_gemv_kernel<Q8_SCALE_ROW>, grid, dim3(GEMV_THREADS), 0, stream, a); break;

@@ -68,6 +68,8 @@ enum GemvEpilogue : int {
     EPI_GEGLU = 4,     // rows interleave gate/up: out[row/2] = mul(gelu(gate), up)
     EPI_ROPE_KV = 5,   // rows q|k|v: rotate q and k pairs at the token's position
                        // (mistral consecutive pairs), q -> out, k/v -> caches
+    EPI_HEAD_SELECT = 6,  // logits = softcap(value) and each tile's first maximum
+                          // to sel_partial, for iris_select_launch
 };
 
 struct GemvArgs {
@@ -88,13 +90,33 @@ struct GemvArgs {
     const int32_t* d_pos;       // absolute position of token 0 of this launch
     const int64_t* inv_freq;    // head_dim/2 Q32.32 angles per position
     uint32_t head_dim, q_rows, kv_rows;
-    int32_t* k_cache;           // [position][kv_rows]
-    int32_t* v_cache;
+    int32_t* k_cache;           // transposed: [kv_rows][k_pos_stride]
+    uint32_t k_pos_stride;
+    int32_t* v_cache;           // [position][kv_rows]
+    // EPI_HEAD_SELECT
+    int32_t* logits_keep;       // [steps][rows] or null
+    int32_t* d_step;
+    int32_t* d_pos_rw;
+    uint32_t rows_in_pass;
+    int32_t* tokens_out;        // [steps]
+    const uint8_t* embed_raw;   // Q8_0 rows, reference layout
+    uint32_t embed_row_bytes, hidden;
+    int32_t embed_scale;        // 0 = unscaled
+    int32_t* x_next;            // [hidden]
+    uint64_t* sel_partial;      // [tiles]: (index << 32) | (uint32)value of each tile's first maximum
 };
+
+// After an EPI_HEAD_SELECT product with the same arguments: selects the first
+// maximum over the tile partials, writes the token, embeds it as the next
+// row and advances step and position.
+int iris_select_launch(const GemvArgs& a, hipStream_t stream);
 
 // Launches the exact Q8_0 product out[t][r] = dot_row(x[t], W[r]) (with the
 // prologue/epilogue) on `stream`. Returns a hipError_t value.
 int iris_gemv_launch(const GemvArgs& a, hipStream_t stream);
+// Reads the device's CU count and raises the product kernels' LDS limit;
+// called before any launch can be captured into a graph.
+void iris_gemv_prepare();
 
 // Packs raw Q8_0 rows (device memory, reference layout) into m's tiled layout
 // and fills its scales; `m` must have its buffers allocated for `mode`.

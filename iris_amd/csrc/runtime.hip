@@ -275,6 +275,7 @@ static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         g.q_rows = qw;
         g.kv_rows = kvw;
         g.k_cache = s->k_cache[l];
+        g.k_pos_stride = s->max_positions;
         g.v_cache = s->v_cache[l];
         RT_CHECK(iris_gemv_launch(g, st));
         // 2. attention.
@@ -282,6 +283,7 @@ static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         a.q = s->q;
         a.q_stride = qw;
         a.k_cache = s->k_cache[l];
+        a.k_pos_stride = s->max_positions;
         a.v_cache = s->v_cache[l];
         a.kv_stride = kvw;
         a.ctx = s->ctx;
@@ -293,6 +295,11 @@ static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         a.scaled = 1;
         a.scale_q32 = d.attention_scale_q32;
         a.window = 0;
+        a.scores = s->attn_scores;
+        a.chunk_max = s->attn_chunk_max;
+        a.chunk_acc = s->attn_chunk_acc;
+        a.chunk_wsum = s->attn_chunk_wsum;
+        a.max_weight = s->attn_max_weight;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 3. attended = W_o ctx + x.
         g = GemvArgs{};
@@ -349,24 +356,23 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     g.prologue = PRO_RMSNORM;
     g.norm_w = m->final_norm;
     g.norm_eps = d.norm_eps;
-    g.epilogue = EPI_STORE;
+    g.epilogue = EPI_HEAD_SELECT;
+    g.softcap = m->head_softcap;
     g.out = s->logits;
     g.out_stride = d.vocab;
+    g.logits_keep = s->keep_logits ? s->logits_keep : nullptr;
+    g.d_step = s->d_step;
+    g.d_pos_rw = s->d_pos;
+    g.rows_in_pass = rows;
+    g.tokens_out = s->tokens;
+    g.embed_raw = m->embed_raw;
+    g.embed_row_bytes = m->embed_row_bytes;
+    g.hidden = d.hidden;
+    g.embed_scale = m->embed_scale;
+    g.x_next = s->x;
+    g.sel_partial = s->sel_partial;
     RT_CHECK(iris_gemv_launch(g, s->stream));
-    SelectArgs a{};
-    a.logits = s->logits;
-    a.vocab = d.vocab;
-    a.tokens_out = s->tokens;
-    a.logits_keep = s->keep_logits ? s->logits_keep : nullptr;
-    a.d_step = s->d_step;
-    a.d_pos = s->d_pos;
-    a.rows_in_pass = rows;
-    a.embed_raw = m->embed_raw;
-    a.row_bytes = m->embed_row_bytes;
-    a.hidden = d.hidden;
-    a.embed_scale = 0;
-    a.x_next = s->x;
-    return iris_select_embed_launch(a, s->stream);
+    return iris_select_launch(g, s->stream);
 }
 
 static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t count) {
@@ -414,6 +420,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     *out = nullptr;
     const IrisModelDesc& d = m->d;
     if (max_rows > max_positions || max_positions > ATTN_MAX_KEYS) return IRIS_E_RANGE;
+    iris_gemv_prepare();
     IrisSession* s = new (std::nothrow) IrisSession();
     if (!s) return IRIS_E_NOMEM;
     s->model = m;
@@ -440,6 +447,14 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->tokens, max_positions + 1);
     alloc(&s->d_pos, 1);
     alloc(&s->d_step, 1);
+    if (st == hipSuccess) st = hipMalloc((void**)&s->sel_partial, (size_t)m->head->tiles * sizeof(uint64_t));
+    const size_t heads = d.heads;
+    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_scores, heads * ATTN_MAX_KEYS * sizeof(int32_t));
+    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_chunk_max, heads * ATTN_MAX_CHUNKS * sizeof(uint64_t));
+    if (st == hipSuccess)
+        st = hipMalloc((void**)&s->attn_chunk_acc, heads * ATTN_MAX_CHUNKS * d.head_dim * sizeof(int64_t));
+    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_chunk_wsum, heads * ATTN_MAX_CHUNKS * sizeof(int32_t));
+    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_max_weight, heads * sizeof(int32_t));
     if (st != hipSuccess) {
         iris_session_free(s);
         return (int)st;
@@ -456,6 +471,12 @@ void iris_session_free(IrisSession* s) {
     for (int32_t* p : {s->x, s->attended, s->q, s->ctx, s->gated, s->logits, s->ids, s->tokens, s->d_pos, s->d_step,
                        s->logits_keep})
         hipFree(p);
+    hipFree(s->sel_partial);
+    hipFree(s->attn_scores);
+    hipFree(s->attn_chunk_max);
+    hipFree(s->attn_chunk_acc);
+    hipFree(s->attn_chunk_wsum);
+    hipFree(s->attn_max_weight);
     if (s->stream) hipStreamDestroy(s->stream);
     delete s;
 }

@@ -33,6 +33,8 @@ struct IrisModel {
     Q8GpuMatrix* head = nullptr;
     int32_t* final_norm = nullptr;
     int64_t* inv_freq = nullptr;
+    int32_t head_softcap = 0;   // 0 = uncapped (mistral-dense)
+    int32_t embed_scale = 0;    // 0 = unscaled (mistral-dense)
     hipStream_t stream = nullptr;
     bool finalized = false;
 };
@@ -48,6 +50,13 @@ struct IrisSession {
     int32_t* logits_keep = nullptr;
     size_t logits_keep_cap = 0;
     bool keep_logits = false;
+    uint64_t* sel_partial = nullptr;
+    // split decode attention scratch
+    int32_t* attn_scores = nullptr;
+    uint64_t* attn_chunk_max = nullptr;
+    int64_t* attn_chunk_acc = nullptr;
+    int32_t* attn_chunk_wsum = nullptr;
+    int32_t* attn_max_weight = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     bool graph_keep_logits = false;
 };
