@@ -1,0 +1,146 @@
+"""Benchmark: exact Q8_0 greedy decode at Mistral-7B shape on one MI355X.
+
+The workload is the north-star decode configuration: 32 mistral-dense layers
+(hidden 4096, 32 query / 8 KV heads of 128, SwiGLU 14336, vocab 32000,
+RoPE base 1e6), random-init Q8_0 weights from a seed, a 512-token prompt and
+greedy decoding at batch 1. One step is one decode pass (every layer and the
+head over one row, then the greedy selection); the timed region is `--steps`
+consecutive steps after the prompt pass, timed with HIP events on the
+session's stream (the weights and KV cache are already resident in HBM).
+
+The JSON line also carries:
+- roofline: the metric's Q8_0 GEMV (M=1, K=4096, N=14336) timed with HIP
+  events over launches that cycle through enough copies of the matrix that
+  each one reads from HBM; algorithmic bytes = weights at 34/32 B each +
+  activations + outputs;
+- decode_roofline: the whole decode step against HBM (weights + KV cache
+  read per token);
+- cpu_baseline: the CPU oracle (a C restatement of the reference's kernels)
+  timed on a bounded sample of the same decode on this host's cores.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tokens/sec + Q8 GEMV HBM GB/s (% peak), bit-exact, 1 MI355X"
+PEAK_HBM_GBPS = 8000.0
+# HBM bytes one launch of the roofline GEMV moves, from rocprofv3 FETCH_SIZE
+# and WRITE_SIZE passes scaled by a 256 MiB device copy (fetch x2.000, write
+# x1.000): profiles/q8_gemv_row_scale_k4096_n14336.md. Re-measure when the
+# kernel or its layout changes.
+GEMV_TRAFFIC_BYTES = 59_278_000
+PROMPT = 512  # the prompt length of the timed workload
+DECODE_TOKENS = 512
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def gemv_roofline(decode_timing):
+    """The metric's GEMV: M=1, K=4096, N=14336, weights one f16 scale per row."""
+    g = decode_timing.time_gemv()
+    achieved = g["algorithmic_bytes"] / (g["us"] * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4), "traffic": GEMV_TRAFFIC_BYTES,
+            "kernel": "q8_gemv_persistent<row scale>", "launch": "Q8_0 GEMV M=1 K=4096 N=14336",
+            "algorithmic_bytes": g["algorithmic_bytes"], "avg_launch_us": round(g["us"], 3)}
+
+
+def cpu_baseline(model, threads, steps=4):
+    """The oracle's decode steps at positions 512.. with a random-filled KV
+    cache (the 512-token prompt pass is not run on the CPU). The oracle is
+    loaded here, after every GPU measurement."""
+    from oracle import cpu
+    run = cpu.OracleRun(model, PROMPT + steps + 1, threads=threads)
+    rng = np.random.default_rng(5)
+    for layer in range(model.num_layers):
+        run.k_cache[layer][:PROMPT] = rng.integers(-(1 << 18), 1 << 18, run.k_cache[layer][:PROMPT].shape)
+        run.v_cache[layer][:PROMPT] = rng.integers(-(1 << 18), 1 << 18, run.v_cache[layer][:PROMPT].shape)
+    tok = 1
+    t0 = time.perf_counter()
+    for i in range(steps):
+        rows, _ = run.pass_rows([tok], PROMPT + i)
+        logits = run.logits(rows[-1])
+        tok = int(np.argmax(logits))
+    dt = time.perf_counter() - t0
+    return {"value": round(steps / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} decode steps of the same model at positions {PROMPT}..{PROMPT + steps - 1} "
+                      f"over a random-filled KV cache (CPU oracle, {threads} threads; prompt pass not run)"}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=DECODE_TOKENS - 1)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--cpu-steps", type=int, default=4)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)",
+              file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or PROMPT + args.steps > 4096:
+        print("--steps must be in 1..3584", file=sys.stderr)
+        sys.exit(2)
+
+    from iris_amd import decode_timing, native, synth
+
+    native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    bench = decode_timing.DecodeBench(max(args.steps, args.warmup), log=log)
+    if args.warmup:
+        bench.run(args.warmup)
+    native.check(native.lib().q8gpu_synchronize(), "synchronize")
+    wall0 = time.perf_counter()
+    ms_per_token, prefill_ms, tokens = bench.run(args.steps)
+    native.check(native.lib().q8gpu_synchronize(), "synchronize")
+    wall = time.perf_counter() - wall0
+    log(f"decode {ms_per_token:.3f} ms/token; prompt pass {prefill_ms:.1f} ms; wall {wall:.2f}s")
+
+    # Determinism: the same decode again gives the same tokens.
+    _, _, tokens2 = bench.run(min(args.steps, 32))
+    deterministic = tokens2 == tokens[:len(tokens2)]
+
+    per_token = bench.bytes_per_step(args.steps)
+    decode_gbps = per_token / (ms_per_token * 1e-3) / 1e9
+
+    roof = gemv_roofline(decode_timing)
+    log(f"GEMV {roof['avg_launch_us']} us = {roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of peak)")
+
+    base = None
+    if not args.no_cpu:
+        threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+        base = cpu_baseline(synth.mistral_7b(seed=decode_timing.MISTRAL_7B_SEED), threads, args.cpu_steps)
+        log(f"CPU oracle: {base['value']} tokens/s on {threads} threads")
+
+    line = {
+        "metric": METRIC, "value": round(1000.0 / ms_per_token, 2), "unit": "tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_token, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8xi32->i64 exact",
+        "data": "synthetic (random-init Q8_0 weights from a seed, uniform prompt ids)",
+        "config": {"workload": "mistral-7b-shape Q8_0 greedy decode, prompt 512 + 512 tokens, batch 1",
+                   "prompt_tokens": PROMPT, "decode_steps_timed": args.steps, "batch": 1},
+        "roofline": roof,
+        "decode_roofline": {"bound": "hbm", "achieved": round(decode_gbps, 1), "peak": PEAK_HBM_GBPS,
+                            "unit": "GB/s", "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
+                            "bytes_per_token": int(per_token)},
+        "prompt_pass_ms": round(prefill_ms, 2),
+        "deterministic_rerun": deterministic,
+        "cpu_baseline": base,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

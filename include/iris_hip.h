@@ -85,6 +85,9 @@ int iris_device_malloc(uint64_t bytes, void** out);
 int iris_device_free(void* ptr);
 int iris_memcpy_h2d(void* dst, const void* src, uint64_t bytes);
 int iris_memcpy_d2h(void* dst, const void* src, uint64_t bytes);
+/* Device-to-device copy (a plain copy kernel of known size, which is what
+ * hardware byte counters are calibrated against). */
+int iris_memcpy_d2d(void* dst, const void* src, uint64_t bytes);
 
 /* Runs q8gpu_product_device `iterations` times back to back on one stream,
  * cycling through `count` matrices of one shape (so that, with enough of

@@ -271,6 +271,10 @@ int iris_memcpy_d2h(void* dst, const void* src, uint64_t bytes) {
     return (int)hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost);
 }
 
+int iris_memcpy_d2d(void* dst, const void* src, uint64_t bytes) {
+    return (int)hipMemcpy(dst, src, bytes, hipMemcpyDeviceToDevice);
+}
+
 int iris_time_product(const Q8GpuMatrix* const* ms, uint32_t count, const int32_t* d_act, uint32_t tokens,
                       int32_t* d_out, uint32_t iterations, double* ms_per_product) {
     if (!ms || count == 0 || !ms_per_product || iterations == 0) return IRIS_E_INVALID;

@@ -385,9 +385,11 @@ static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t 
     return iris_embed_rows_launch(s->ids, count, m->embed_raw, m->embed_row_bytes, m->d.hidden, 0, s->x, s->stream);
 }
 
-// Captures the decode pass (one row, head, select) as a graph once.
-static int ensure_graph(IrisSession* s) {
-    if (s->graph_exec && s->graph_keep_logits == s->keep_logits) return 0;
+// Captures the decode pass (one row, head, select) as a graph. Each
+// generation captures its own (a few hundred nodes, outside any timed
+// region), so no graph outlives the call that made it.
+static int ensure_graph(IrisSession* s, bool fresh) {
+    if (!fresh && s->graph_exec && s->graph_keep_logits == s->keep_logits) return 0;
     if (s->graph_exec) {
         hipGraphExecDestroy(s->graph_exec);
         s->graph_exec = nullptr;
@@ -409,7 +411,7 @@ static int session_decode_pass(IrisSession* s, int use_graph) {
         RT_CHECK(session_pass(s, 1, nullptr));
         return session_head_select(s, 1);
     }
-    RT_CHECK(ensure_graph(s));
+    RT_CHECK(ensure_graph(s, false));
     return (int)hipGraphLaunch(s->graph_exec, s->stream);
 }
 
@@ -507,6 +509,7 @@ int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt
     RT_CHECK(session_reset_and_embed(s, prompt, prompt_len));
     RT_CHECK(session_pass(s, prompt_len, nullptr));
     RT_CHECK(session_head_select(s, prompt_len));
+    if (use_graph && tokens > 1) RT_CHECK(ensure_graph(s, true));
     for (uint32_t t = 1; t < tokens; t++) RT_CHECK(session_decode_pass(s, use_graph));
     RT_CHECK(hipMemcpyAsync(out_tokens, s->tokens, (size_t)tokens * 4, hipMemcpyDeviceToHost, s->stream));
     if (out_logits)
@@ -572,7 +575,7 @@ int iris_session_time_decode(IrisSession* s, const int32_t* prompt, uint32_t pro
     if (rc == 0) rc = session_head_select(s, prompt_len);
     // Capture (outside the timed region) before timing the replays.
     if (rc == 0) rc = (int)hipEventRecord(e1, s->stream);
-    if (rc == 0) rc = ensure_graph(s);
+    if (rc == 0) rc = ensure_graph(s, true);
     float pre = 0.f, dec = 0.f;
     if (rc == 0) rc = (int)hipEventSynchronize(e1);
     if (rc == 0) rc = (int)hipEventElapsedTime(&pre, e0, e1);

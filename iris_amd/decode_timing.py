@@ -1,0 +1,134 @@
+"""Device-side timing of the exact decode loop and of its Q8_0 GEMV.
+
+Both measurements run entirely on the GPU with HIP events on the stream the
+kernels are launched on; the weights, KV cache and activations are resident
+in HBM before the timed region starts.
+
+`python -m iris_amd.decode_timing [--steps K] [--warmup W]` prints one JSON
+line with the same figures the benchmark reports, so the kernels it launches
+can be traced on their own (for example under `rocprofv3 --kernel-trace
+--stats`).
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes as C
+import json
+import sys
+
+import numpy as np
+
+from . import native, synth
+from .direct import DeviceModel, Session
+
+PROMPT = 512
+MISTRAL_7B_SEED = 0x7B7B
+PROMPT_SEED = 0x5EED
+# Q8_0 bytes of every product one decode step reads at Mistral-7B shape:
+# 32 x (q|k|v 6144 + o 4096 + gate|up 28672 + down 4096 rows) x K + head.
+MISTRAL_7B_WEIGHT_BYTES = 7554793472
+
+GEMV_N, GEMV_K = 14336, 4096
+
+
+def gemv_algorithmic_bytes(n: int = GEMV_N, k: int = GEMV_K) -> int:
+    """Q8_0 weights (34 bytes per 32 values) + i32 activations + i32 outputs."""
+    return n * k * 34 // 32 + k * 4 + n * 4
+
+
+def copy_calibration(mib: int = 256, repeats: int = 3) -> int:
+    """Device-to-device copies of `mib` MiB, `repeats` times: a plain copy
+    kernel of known size (each dispatch reads and writes exactly mib MiB),
+    against which hardware byte counters such as FETCH_SIZE and WRITE_SIZE
+    are scaled."""
+    n = mib << 20
+    src, dst = native.DeviceBuffer(n), native.DeviceBuffer(n)
+    for _ in range(repeats):
+        native.check(native.lib().iris_memcpy_d2d(dst.ptr, src.ptr, n), "copy")
+    return n
+
+
+def time_gemv(iterations: int = 200, n: int = GEMV_N, k: int = GEMV_K) -> dict:
+    """Average duration of one Q8_0 GEMV launch (M=1) with one f16 scale per
+    row. Launches cycle through enough copies of the matrix (more than 600 MB
+    in all) that each reads its weights from HBM, not from the 256 MB
+    Infinity Cache."""
+    from .tensor import Q8Matrix
+
+    raw = synth.q8_matrix(synth.tensor_seed(2, 1), n, k, synth.scale_base_for(k), True)
+    copies = max(1, -(-600_000_000 // (n * k * 34 // 32)))
+    mats = [Q8Matrix.from_bytes(raw, n, k) for _ in range(copies)]
+    arr = (C.c_void_p * copies)(*[m.handle.value for m in mats])
+    rng = np.random.default_rng(2)
+    x = (rng.integers(-127, 128, (1, k)) * (256 + int(rng.integers(0, 256)))).astype(np.int32)
+    dx = native.DeviceBuffer.from_array(x)
+    dout = native.DeviceBuffer(n * 4)
+    ms = C.c_double()
+    native.check(native.lib().iris_time_product(arr, copies, dx.ptr, 1, dout.ptr, iterations, C.byref(ms)),
+                 "time GEMV")
+    for m in mats:
+        m.free()
+    return {"us": ms.value * 1e3, "copies": copies, "n": n, "k": k,
+            "algorithmic_bytes": gemv_algorithmic_bytes(n, k)}
+
+
+class DecodeBench:
+    """Mistral-7B-shape model on the device with a session sized for a
+    512-token prompt followed by `max_steps` decode steps."""
+
+    def __init__(self, max_steps: int, log=None):
+        import time
+        log = log or (lambda msg: None)
+        t = time.time()
+        model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
+        log(f"weights generated in {time.time() - t:.1f}s")
+        t = time.time()
+        self.dm = DeviceModel(model)
+        log(f"uploaded in {time.time() - t:.1f}s")
+        self.shape = model.shape
+        self.vocab = model.vocab
+        del model.tensors  # the device holds the weights now
+        self.session = Session(self.dm, PROMPT + max_steps + 1, PROMPT)
+        self.prompt = synth.token_ids(PROMPT_SEED, PROMPT, self.vocab)
+
+    def run(self, steps: int):
+        """(ms per decode step, prompt-pass ms, token ids) for one timed
+        decode of `steps` steps after the prompt pass."""
+        return self.session.time_decode(self.prompt, steps)
+
+    def bytes_per_step(self, steps: int) -> float:
+        """HBM bytes one decode step must read: every weight once plus the
+        K and V caches up to the step's position (averaged over the run)."""
+        s = self.shape
+        kvw = s.num_key_value_heads * s.head_dim
+        mean_ctx = PROMPT + (steps + 1) / 2.0
+        return MISTRAL_7B_WEIGHT_BYTES + 2 * 4 * kvw * s.num_hidden_layers * mean_ctx
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
+    ap.add_argument("--steps", type=int, default=PROMPT - 1)
+    ap.add_argument("--warmup", type=int, default=8)
+    ap.add_argument("--gemv-only", action="store_true", help="time only the Q8_0 GEMV")
+    ap.add_argument("--calibrate", action="store_true",
+                    help="first run a 256 MiB device-to-device copy (byte-counter calibration)")
+    args = ap.parse_args(argv)
+    native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    if args.calibrate:
+        copy_calibration()
+    if args.gemv_only:
+        g = time_gemv()
+        print(json.dumps({"gemv_us": round(g["us"], 3), "gemv_copies": g["copies"],
+                          "algorithmic_bytes": g["algorithmic_bytes"]}), flush=True)
+        return
+    bench = DecodeBench(max(args.steps, args.warmup), log=lambda m: print(m, file=sys.stderr, flush=True))
+    if args.warmup:
+        bench.run(args.warmup)
+    ms, prefill, _ = bench.run(args.steps)
+    g = time_gemv()
+    print(json.dumps({"decode_ms_per_step": round(ms, 4), "prompt_pass_ms": round(prefill, 2),
+                      "gemv_us": round(g["us"], 3), "gemv_copies": g["copies"]}), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -66,6 +66,7 @@ def _declare(L):
         "iris_device_free": (C.c_int, [vp]),
         "iris_memcpy_h2d": (C.c_int, [vp, vp, u64]),
         "iris_memcpy_d2h": (C.c_int, [vp, vp, u64]),
+        "iris_memcpy_d2d": (C.c_int, [vp, vp, u64]),
         "iris_time_product": (C.c_int, [vp, u32, vp, u32, vp, u32, C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
