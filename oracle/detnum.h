@@ -10,6 +10,14 @@
  * Types follow det-num: Act = Q16.16 in int32_t, Acc = Q32.32 in int64_t,
  * Q8_0 blocks = 2-byte little-endian f16 scale + 32 signed bytes.
  * Every function cites the reference function it restates.
+ *
+ * Pinning: the rounding, saturation, MAC, f32->fixed, scale_q24, dot_row,
+ * RoPE, attention-scale, YaRN and SiLU special values are pinned by the
+ * reference's own test vectors; inv_sqrt_acc by exhaustive neighbour checks.
+ * Parity unpinned at the last bit: softmax_exp_term, tanh/gelu/softcap,
+ * sin_cos_acc, nth_root_acc, sin_cos_q30 and exp_neg_q32/sigmoid_q32 are
+ * checked only against their truncation-error bounds around the real
+ * functions (no reference vectors exist for them).
  */
 #ifndef IRIS_ORACLE_DETNUM_H
 #define IRIS_ORACLE_DETNUM_H

@@ -8,6 +8,12 @@
  * are the reference's raw bytes, rows of cols/32 blocks of 34 bytes; a key
  * cache is int32 [positions][kv_heads*head_dim], one row per position.
  * All functions return 0 on success and a negative code on a malformed input.
+ *
+ * Parity unpinned: the reference holds no expected outputs for a whole layer,
+ * the head or a generation, and its Rust source cannot be built here. The
+ * layer forwards, orc_gemma_ple_prepare and orc_head_logits are pinned only
+ * by structural invariants (batched prefill == chunked decode, the per-value
+ * products equal dot_row) and by the det-num pieces they compose.
  */
 #ifndef IRIS_ORACLE_LAYERS_H
 #define IRIS_ORACLE_LAYERS_H
