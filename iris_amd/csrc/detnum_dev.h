@@ -97,6 +97,39 @@ __device__ __forceinline__ int64_t acc_mul(int64_t a, int64_t b) {
     return clamp_i128_to_i64(r);
 }
 
+// ops.rs:67-78: round-half-even of (n << 32) / d, clamped.
+__device__ inline int64_t div_acc(int64_t n, int64_t d) {
+    return clamp_i128_to_i64(rte_div_i128((i128)n * ((i128)1 << 32), (i128)d));
+}
+
+// ops.rs:608-614: base^exponent by repeated acc_mul, from ONE.
+__device__ inline int64_t pow_acc_u32(int64_t base, uint32_t exponent) {
+    int64_t r = ONE_ACC;
+    for (uint32_t i = 0; i < exponent; i++) r = acc_mul(r, base);
+    return r;
+}
+
+// ops.rs:564-606: the Q32.32 value whose degree-th power is closest to
+// `value` (binary search for the largest r with r^degree <= value, then the
+// nearer of r and r + 1, ties to the even one).
+__device__ inline int64_t nth_root_acc(int64_t value, uint32_t degree) {
+    if (degree == 1 || value == ONE_ACC) return value;
+    int64_t low = 0, high = value > ONE_ACC ? value : ONE_ACC;
+    while (low < high) {
+        const int64_t mid = low + (high - low + 1) / 2;
+        if (pow_acc_u32(mid, degree) <= value) low = mid;
+        else high = mid - 1;
+    }
+    const int64_t lower = low, upper = lower == INT64_MAX ? INT64_MAX : lower + 1;
+    i128 le = (i128)value - pow_acc_u32(lower, degree);
+    i128 ue = (i128)pow_acc_u32(upper, degree) - value;
+    if (le < 0) le = -le;
+    if (ue < 0) ue = -ue;
+    if (ue < le) return upper;
+    if (le < ue) return lower;
+    return (lower & 1) == 0 ? lower : upper;
+}
+
 // ops.rs:67-78 div_acc for the softmax's case: numerator in [0, 2^32] and
 // denominator >= numerator > 0, so the 96-bit dividend e * 2^32 <= 2^64 is
 // handled with one 64-bit division (the 2^64 edge by its predecessor).

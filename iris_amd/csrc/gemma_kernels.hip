@@ -1,0 +1,215 @@
+// The gemma-dense layer's kernels that are not Q8_0 products:
+//  - the per-head q/k rms_norm + RoPE and v value-norm after the q|k|v
+//    product, with the K/V cache store (prefill_range.rs:607-647);
+//  - rms_norm of a product's rows followed by the residual add (the post
+//    norms, prefill_range.rs:879-958);
+//  - products with Q16.16 matrices, dot_bits rows (tensor.rs:522-528), for
+//    the per-layer-input (PLE) gate and projection;
+//  - the PLE prepare step of every layer (view_kernels.rs:59-99);
+//  - the RoPE frequency ladder (ops.rs:154-199, 558-620), built once.
+#include "detnum_dev.h"
+#include "layer_kernels.h"
+
+namespace {
+
+constexpr uint32_t NT = 256;  // threads per workgroup in this file
+constexpr uint32_t NW = NT / 64;
+
+__device__ __forceinline__ int64_t wave_sum_sat(int64_t v) {
+    for (int off = 32; off >= 1; off >>= 1) v = dn::acc_add_sat(v, __shfl_xor(v, off));
+    return v;
+}
+
+// Saturating sum of non-negative terms over the workgroup (order-free:
+// the result is min(true sum, i64::MAX) whatever the order).
+__device__ __forceinline__ int64_t block_sum_sat(int64_t v, int64_t* s_red) {
+    const uint32_t tid = threadIdx.x;
+    v = wave_sum_sat(v);
+    if ((tid & 63) == 0) s_red[tid >> 6] = v;
+    __syncthreads();
+    int64_t t = 0;
+    for (uint32_t i = 0; i < NW; i++) t = dn::acc_add_sat(t, s_red[i]);
+    __syncthreads();  // s_red may be reused by the caller
+    return t;
+}
+
+// One head of one row per workgroup. Heads [0, heads) are queries,
+// [heads, heads+kv_heads) keys, then values, as the q|k|v product stacks
+// them. q, k: rms_norm with their weights, then RoPE on pairs
+// (i, i + rotary/2); v: the weightless value norm (ops.rs:124-134).
+__global__ __launch_bounds__(NT) void gemma_qkv_finish_kernel(const GemmaQkvArgs a) {
+    __shared__ int32_t s_v[GEMMA_MAX_HEAD_DIM];
+    __shared__ int64_t s_red[NW];
+    const uint32_t h = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const uint32_t hd = a.head_dim;
+    const int32_t* src = a.qkv + (size_t)t * a.qkv_stride + (size_t)h * hd;
+    int64_t ss = 0;
+    for (uint32_t i = tid; i < hd; i += NT) {
+        const int32_t v = src[i];
+        s_v[i] = v;
+        ss = dn::acc_add_sat(ss, (int64_t)v * v);
+    }
+    const int32_t scale = dn::rms_scale_from_sum(block_sum_sat(ss, s_red), hd, a.eps);
+    const bool is_q = h < a.heads, is_k = !is_q && h < a.heads + a.kv_heads;
+    const int32_t* nw = is_q ? a.q_norm : a.k_norm;
+    for (uint32_t i = tid; i < hd; i += NT)
+        s_v[i] = (is_q || is_k) ? dn::mul_sat(dn::mul_sat(s_v[i], scale), nw[i]) : dn::mul_sat(s_v[i], scale);
+    __syncthreads();
+    const uint32_t pos = (uint32_t)(*a.d_pos) + t;
+    if ((is_q || is_k) && pos != 0 && a.rotary_dim != 0) {
+        const uint32_t half = a.rotary_dim / 2;
+        for (uint32_t i = tid; i < half; i += NT) {
+            // mul_usize_by_acc (ops.rs:616-620): position * inv_f, clamped.
+            const int64_t angle = dn::clamp_i128_to_i64((dn::i128)pos * (dn::i128)a.inv_freq[i]);
+            int32_t c, s;
+            dn::sin_cos_acc(angle, c, s);
+            const int32_t lhs = s_v[i], rhs = s_v[i + half];
+            s_v[i] = dn::sub_sat(dn::mul_sat(lhs, c), dn::mul_sat(rhs, s));
+            s_v[i + half] = dn::add_sat(dn::mul_sat(rhs, c), dn::mul_sat(lhs, s));
+        }
+        __syncthreads();
+    }
+    if (is_q) {
+        int32_t* dst = a.q_out + (size_t)t * a.q_stride + (size_t)h * hd;
+        for (uint32_t i = tid; i < hd; i += NT) dst[i] = s_v[i];
+    } else if (is_k) {
+        const size_t kbase = (size_t)(h - a.heads) * hd;
+        for (uint32_t i = tid; i < hd; i += NT) a.k_cache[(kbase + i) * a.k_pos_stride + pos] = s_v[i];
+    } else {
+        const size_t vbase = (size_t)(h - a.heads - a.kv_heads) * hd;
+        int32_t* dst = a.v_cache + (size_t)pos * ((size_t)a.kv_heads * hd) + vbase;
+        for (uint32_t i = tid; i < hd; i += NT) dst[i] = s_v[i];
+    }
+}
+
+// out = add_sat(rms_norm(a, w), res), then mul_sat(., scalar) when scalar is
+// set (the layer scalar, prefill_range.rs:946-958). One row per workgroup;
+// out may be res (each element is read and written by one thread).
+__global__ __launch_bounds__(NT) void norm_residual_kernel(const int32_t* a, uint32_t a_stride, const int32_t* w,
+                                                           int64_t eps, const int32_t* res, uint32_t res_stride,
+                                                           int32_t scalar, int32_t* out, uint32_t out_stride,
+                                                           uint32_t n) {
+    __shared__ int64_t s_red[NW];
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const int32_t* ar = a + (size_t)t * a_stride;
+    int64_t ss = 0;
+    for (uint32_t i = tid; i < n; i += NT) ss = dn::acc_add_sat(ss, (int64_t)ar[i] * ar[i]);
+    const int32_t scale = dn::rms_scale_from_sum(block_sum_sat(ss, s_red), n, eps);
+    const int32_t* rr = res + (size_t)t * res_stride;
+    int32_t* orow = out + (size_t)t * out_stride;
+    for (uint32_t i = tid; i < n; i += NT) {
+        int32_t v = dn::add_sat(dn::mul_sat(dn::mul_sat(ar[i], scale), w[i]), rr[i]);
+        if (scalar != 0) v = dn::mul_sat(v, scalar);
+        orow[i] = v;
+    }
+}
+
+// out[t][r] = requantize(wrapping sum_k x[t][k] * W[r][k]) for a Q16.16
+// matrix W [rows][cols] (dot_bits, tensor.rs:522-528; mac_bits ops.rs:17-19),
+// optionally followed by mul_sat(gelu(.), aux[t][r]) (the PLE gate,
+// prefill_range.rs:931-944). One row per wave, four rows per workgroup.
+__global__ __launch_bounds__(NT) void i32_gemv_kernel(const I32GemvArgs a) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t row = blockIdx.x * NW + wave, t = blockIdx.y;
+    if (row >= a.rows) return;
+    const int32_t* xr = a.x + (size_t)t * a.x_stride;
+    const int32_t* wr = a.w + (size_t)row * a.cols;
+    uint64_t acc = 0;
+    for (uint32_t k = lane * 4; k < a.cols; k += 256) {
+        const int4 xv = *(const int4*)(xr + k);
+        const int4 wv = *(const int4*)(wr + k);
+        acc += (uint64_t)((int64_t)xv.x * wv.x);
+        acc += (uint64_t)((int64_t)xv.y * wv.y);
+        acc += (uint64_t)((int64_t)xv.z * wv.z);
+        acc += (uint64_t)((int64_t)xv.w * wv.w);
+    }
+    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
+    if (lane == 0) {
+        int32_t v = dn::requantize((int64_t)acc);
+        if (a.aux) v = dn::mul_sat(dn::gelu(v), a.aux[(size_t)t * a.aux_stride + row]);
+        a.out[(size_t)t * a.out_stride + row] = v;
+    }
+}
+
+// The PLE input of one layer segment for one row (view_kernels.rs:74-88):
+// p = rms_norm(mul_sat(proj, projection_scalar), norm); e = the token's
+// dequantized embed_tokens_per_layer columns of the segment, times the
+// embedding scale; out = mul_sat(add_sat(e, p), input_scale).
+__global__ __launch_bounds__(NT) void ple_prepare_kernel(const PleArgs a) {
+    __shared__ int32_t s_p[GEMMA_MAX_PLE];
+    __shared__ int64_t s_red[NW];
+    const uint32_t seg = blockIdx.x, t = blockIdx.y, tid = threadIdx.x;
+    const uint32_t P = a.ple_width;
+    const int32_t* pr = a.proj + (size_t)t * a.row_stride + (size_t)seg * P;
+    int64_t ss = 0;
+    for (uint32_t c = tid; c < P; c += NT) {
+        const int32_t p = dn::mul_sat(pr[c], a.projection_scalar);
+        s_p[c] = p;
+        ss = dn::acc_add_sat(ss, (int64_t)p * p);
+    }
+    const int32_t scale = dn::rms_scale_from_sum(block_sum_sat(ss, s_red), P, a.eps);
+    const uint8_t* er = a.emb + (size_t)a.ids[t] * a.emb_row_bytes;
+    int32_t* orow = a.out + (size_t)t * a.row_stride + (size_t)seg * P;
+    for (uint32_t c = tid; c < P; c += NT) {
+        const int32_t p = dn::mul_sat(dn::mul_sat(s_p[c], scale), a.norm_w[c]);
+        const uint32_t col = seg * P + c;
+        const uint8_t* blk = er + (size_t)(col / 32) * 34;
+        const int64_t sc = dn::scale_q24((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
+        int32_t e = dn::round_to_i32((dn::i128)((int64_t)(int8_t)blk[2 + col % 32] * sc), 8);
+        e = dn::add_sat(dn::mul_sat(e, a.embedding_scale), p);
+        orow[c] = dn::mul_sat(e, a.input_scale);
+    }
+}
+
+// inv_f[i] for i < half: ONE, then repeated acc_mul by
+// step = div_acc(ONE, nth_root(base, freq_base_dim / 2)) (ops.rs:154-199,
+// 558-562). Sequential by definition; one thread, once per model.
+__global__ void rope_ladder_kernel(int64_t base, uint32_t freq_base_dim, uint32_t half, int64_t* out) {
+    if (threadIdx.x != 0 || blockIdx.x != 0) return;
+    const int64_t step = dn::div_acc(dn::ONE_ACC, dn::nth_root_acc(base, freq_base_dim / 2));
+    int64_t f = dn::ONE_ACC;
+    for (uint32_t i = 0; i < half; i++) {
+        out[i] = f;
+        f = dn::acc_mul(f, step);
+    }
+}
+
+}  // namespace
+
+int iris_gemma_qkv_finish_launch(const GemmaQkvArgs& a, uint32_t rows, hipStream_t stream) {
+    if (a.head_dim == 0 || a.head_dim > GEMMA_MAX_HEAD_DIM || a.rotary_dim > a.head_dim || a.rotary_dim % 2)
+        return IRIS_E_INVALID;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(gemma_qkv_finish_kernel, dim3(a.heads + 2 * a.kv_heads, rows), dim3(NT), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
+int iris_norm_residual_launch(const int32_t* a, uint32_t a_stride, const int32_t* w, int64_t eps, const int32_t* res,
+                              uint32_t res_stride, int32_t scalar, int32_t* out, uint32_t out_stride, uint32_t n,
+                              uint32_t rows, hipStream_t stream) {
+    if (n == 0) return IRIS_E_INVALID;
+    if (rows == 0) return 0;
+    hipLaunchKernelGGL(norm_residual_kernel, dim3(rows), dim3(NT), 0, stream, a, a_stride, w, eps, res, res_stride,
+                       scalar, out, out_stride, n);
+    return (int)hipGetLastError();
+}
+
+int iris_i32_gemv_launch(const I32GemvArgs& a, uint32_t tokens, hipStream_t stream) {
+    if (a.rows == 0 || a.cols == 0 || a.cols % 4 || a.x_stride % 4) return IRIS_E_INVALID;
+    if (tokens == 0) return 0;
+    hipLaunchKernelGGL(i32_gemv_kernel, dim3((a.rows + NW - 1) / NW, tokens), dim3(NT), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
+int iris_ple_prepare_launch(const PleArgs& a, uint32_t segments, uint32_t rows, hipStream_t stream) {
+    if (a.ple_width == 0 || a.ple_width > GEMMA_MAX_PLE) return IRIS_E_INVALID;
+    if (rows == 0 || segments == 0) return 0;
+    hipLaunchKernelGGL(ple_prepare_kernel, dim3(segments, rows), dim3(NT), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
+int iris_rope_ladder_launch(int64_t base, uint32_t freq_base_dim, uint32_t half, int64_t* out, hipStream_t stream) {
+    if (half == 0) return 0;
+    hipLaunchKernelGGL(rope_ladder_kernel, dim3(1), dim3(64), 0, stream, base, freq_base_dim, half, out);
+    return (int)hipGetLastError();
+}

@@ -37,3 +37,56 @@ constexpr uint32_t ATTN_MAX_CHUNKS = ATTN_MAX_KEYS / ATTN_CHUNK;
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
 int iris_embed_rows_launch(const int32_t* d_ids, uint32_t count, const uint8_t* embed_raw, uint32_t row_bytes,
                            uint32_t hidden, int32_t scale, int32_t* out, hipStream_t stream);
+
+// ---- gemma-dense (gemma_kernels.hip) ----
+
+constexpr uint32_t GEMMA_MAX_HEAD_DIM = ATTN_MAX_HEAD_DIM;
+constexpr uint32_t GEMMA_MAX_PLE = 4096;
+
+struct GemmaQkvArgs {
+    const int32_t* qkv;      // [rows][(heads + 2*kv_heads) * head_dim], the raw q|k|v products
+    uint32_t qkv_stride;
+    uint32_t heads, kv_heads, head_dim, rotary_dim;
+    const int32_t* q_norm;   // [head_dim]
+    const int32_t* k_norm;   // [head_dim]
+    int64_t eps;             // Q32.32
+    const int64_t* inv_freq; // [rotary_dim / 2] Q32.32
+    const int32_t* d_pos;    // absolute position of row 0
+    int32_t* q_out;          // [rows][heads*head_dim]
+    uint32_t q_stride;
+    int32_t* k_cache;        // transposed: [kv_heads*head_dim][k_pos_stride]
+    uint32_t k_pos_stride;
+    int32_t* v_cache;        // [position][kv_heads*head_dim]
+};
+
+struct I32GemvArgs {
+    const int32_t* w;        // Q16.16 [rows][cols], cols % 4 == 0
+    uint32_t rows, cols;
+    const int32_t* x;        // [tokens][x_stride]
+    uint32_t x_stride;
+    int32_t* out;            // [tokens][out_stride]
+    uint32_t out_stride;
+    const int32_t* aux;      // nullable: out = mul_sat(gelu(dot), aux[t][r])
+    uint32_t aux_stride;
+};
+
+struct PleArgs {
+    const int32_t* proj;     // [rows][row_stride]: dot_bits of the projection, all segments
+    uint32_t row_stride;     // layers * ple_width
+    const int32_t* ids;      // [rows] token ids
+    const uint8_t* emb;      // embed_tokens_per_layer, Q8_0 rows of row_stride values
+    uint32_t emb_row_bytes;
+    uint32_t ple_width;
+    const int32_t* norm_w;   // per_layer_projection_norm [ple_width]
+    int64_t eps;
+    int32_t projection_scalar, embedding_scale, input_scale;
+    int32_t* out;            // [rows][row_stride]
+};
+
+int iris_gemma_qkv_finish_launch(const GemmaQkvArgs& a, uint32_t rows, hipStream_t stream);
+int iris_norm_residual_launch(const int32_t* a, uint32_t a_stride, const int32_t* w, int64_t eps, const int32_t* res,
+                              uint32_t res_stride, int32_t scalar, int32_t* out, uint32_t out_stride, uint32_t n,
+                              uint32_t rows, hipStream_t stream);
+int iris_i32_gemv_launch(const I32GemvArgs& a, uint32_t tokens, hipStream_t stream);
+int iris_ple_prepare_launch(const PleArgs& a, uint32_t segments, uint32_t rows, hipStream_t stream);
+int iris_rope_ladder_launch(int64_t base, uint32_t freq_base_dim, uint32_t half, int64_t* out, hipStream_t stream);

@@ -158,6 +158,7 @@ __global__ __launch_bounds__(256) void select_embed_kernel(const GemvArgs a) {
     if (tid == 0) {
         const int32_t step = *a.d_step;
         a.tokens_out[step] = (int32_t)token;
+        if (a.ids_next) a.ids_next[0] = (int32_t)token;
         *a.d_step = step + 1;
         *a.d_pos_rw = *a.d_pos_rw + (int32_t)a.rows_in_pass;
     }

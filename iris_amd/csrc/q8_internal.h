@@ -103,6 +103,7 @@ struct GemvArgs {
     uint32_t embed_row_bytes, hidden;
     int32_t embed_scale;        // 0 = unscaled
     int32_t* x_next;            // [hidden]
+    int32_t* ids_next;          // nullable: the selected id is also stored here
     uint64_t* sel_partial;      // [tiles]: (index << 32) | (uint32)value of each tile's first maximum
 };
 

@@ -14,6 +14,7 @@
 // kernel selects the first maximum and embeds the next row. Positions and
 // the step counter live in device memory, so a decode pass is the same
 // launch sequence every time and is captured once as a HIP graph.
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -106,12 +107,27 @@ int iris_model_create(const IrisModelDesc* desc, IrisModel** out) {
     if (!desc || !out) return IRIS_E_INVALID;
     *out = nullptr;
     const IrisModelDesc& d = *desc;
-    if (d.family != IRIS_FAMILY_MISTRAL_DENSE) return IRIS_E_INVALID;
+    const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
+    if (d.family != IRIS_FAMILY_MISTRAL_DENSE && !gemma) return IRIS_E_INVALID;
     if (!d.hidden || !d.layers || !d.heads || !d.kv_heads || !d.head_dim || !d.ffn || !d.vocab) return IRIS_E_INVALID;
     if (d.heads % d.kv_heads || d.head_dim % 4 || d.hidden % 32 || d.norm_eps < 0) return IRIS_E_INVALID;
+    if (d.head_dim > ATTN_MAX_HEAD_DIM) return IRIS_E_INVALID;
+    if (gemma) {
+        const uint32_t ghd = d.global_head_dim ? d.global_head_dim : d.head_dim;
+        // The PLE segments are whole Q8_0 blocks of embed_tokens_per_layer.
+        if (ghd % 4 || ghd > ATTN_MAX_HEAD_DIM || !d.ple_width || d.ple_width % 32 || d.ple_width > GEMMA_MAX_PLE)
+            return IRIS_E_INVALID;
+        if (d.num_kv_shared_layers > d.layers || d.partial_rotary_q16 < 0 || d.partial_rotary_q16 > 65536)
+            return IRIS_E_INVALID;
+    }
     IrisModel* m = new (std::nothrow) IrisModel();
     if (!m) return IRIS_E_NOMEM;
     m->d = d;
+    if (gemma) {
+        if (!m->d.global_head_dim) m->d.global_head_dim = d.head_dim;
+        m->head_softcap = d.final_logit_softcap;
+        m->embed_scale = d.embedding_scale;
+    }
     m->layer_is_sliding.assign(d.layers, 0);
     if (d.layer_is_sliding) m->layer_is_sliding.assign(d.layer_is_sliding, d.layer_is_sliding + d.layers);
     m->d.layer_is_sliding = nullptr;
@@ -147,10 +163,36 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
     if (layer >= 0) {
         if ((uint32_t)layer >= d.layers) return IRIS_E_INVALID;
         LayerWeights& L = m->layers[layer];
-        if (width == 32 && (suffix == "input_layernorm.weight" || suffix == "pre_feedforward_layernorm.weight")) {
-            if (rows * cols != d.hidden) return IRIS_E_INVALID;
-            int32_t** dst = suffix == "input_layernorm.weight" ? &L.norm_attn : &L.norm_ff;
-            RT_CHECK(dev_alloc_copy(dst, data, bytes));
+        if (width == 32) {
+            const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
+            const uint32_t hd = m->layer_is_sliding[layer] ? d.head_dim : d.global_head_dim;
+            struct {
+                const char* name;
+                int32_t** dst;
+                uint64_t count;
+                bool gemma_only;
+            } vecs[] = {
+                {"input_layernorm.weight", &L.norm_attn, d.hidden, false},
+                {"pre_feedforward_layernorm.weight", &L.norm_ff, d.hidden, false},
+                {"post_attention_layernorm.weight", &L.norm_post_attn, d.hidden, true},
+                {"post_feedforward_layernorm.weight", &L.norm_post_ffw, d.hidden, true},
+                {"post_per_layer_input_norm.weight", &L.norm_post_ple, d.hidden, true},
+                {"self_attn.q_norm.weight", &L.q_norm, hd, true},
+                {"self_attn.k_norm.weight", &L.k_norm, hd, true},
+                {"per_layer_input_gate.weight", &L.ple_gate, (uint64_t)d.ple_width * d.hidden, true},
+                {"per_layer_projection.weight", &L.ple_proj, (uint64_t)d.hidden * d.ple_width, true},
+            };
+            for (auto& v : vecs) {
+                if (suffix != v.name || (v.gemma_only && !gemma)) continue;
+                if (rows * cols != v.count) return IRIS_E_INVALID;
+                if (*v.dst) return IRIS_E_STATE;
+                RT_CHECK(dev_alloc_copy(v.dst, data, bytes));
+                return 0;
+            }
+            if (gemma && suffix == "layer_scalar") {
+                if (rows * cols != 1) return IRIS_E_INVALID;
+                L.layer_scalar = *(const int32_t*)data;
+            }
             return 0;
         }
         if (width != 8) return 0;  // tensors the family does not read are ignored
@@ -189,6 +231,25 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
         RT_CHECK(dev_alloc_copy(&m->final_norm, data, bytes));
         return 0;
     }
+    if (d.family == IRIS_FAMILY_GEMMA_DENSE) {
+        const uint64_t lp = (uint64_t)d.layers * d.ple_width;
+        if (name == std::string(PREFIX) + "embed_tokens_per_layer.weight") {
+            if (width != 8 || rows != d.vocab || cols != lp) return IRIS_E_INVALID;
+            RT_CHECK(dev_alloc_copy(&m->embed_ple, data, bytes));
+            m->embed_ple_row_bytes = (uint32_t)(cols / 32 * 34);
+            return 0;
+        }
+        if (name == std::string(PREFIX) + "per_layer_model_projection.weight") {
+            if (width != 32 || rows * cols != lp * d.hidden) return IRIS_E_INVALID;
+            RT_CHECK(dev_alloc_copy(&m->ple_model_proj, data, bytes));
+            return 0;
+        }
+        if (name == std::string(PREFIX) + "per_layer_projection_norm.weight") {
+            if (width != 32 || rows * cols != d.ple_width) return IRIS_E_INVALID;
+            RT_CHECK(dev_alloc_copy(&m->ple_proj_norm, data, bytes));
+            return 0;
+        }
+    }
     if (name == "rope_inverse_frequencies") {
         if (width != 64 || rows * cols != d.head_dim / 2) return IRIS_E_INVALID;
         const int64_t* f = (const int64_t*)data;
@@ -200,17 +261,77 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
     return 0;
 }
 
+// The per-layer derivations of a gemma-dense model
+// (crates/inference/direct/src/model.rs:817-877): head size, RoPE and
+// window by layer kind, the KV donor of the shared layers, and the two RoPE
+// frequency ladders (validated as prefill_range.rs:394-466 does).
+static int gemma_finalize(IrisModel* m) {
+    const IrisModelDesc& d = m->d;
+    if (!m->embed_ple || !m->ple_model_proj || !m->ple_proj_norm) return IRIS_E_STATE;
+    const uint32_t rot_full = (uint32_t)(((uint64_t)d.global_head_dim * (uint32_t)d.partial_rotary_q16) >> 16);
+    struct Kind {
+        int64_t base;
+        uint32_t hd, rotary;
+        int64_t** table;
+    } kinds[2] = {{d.rope_base_full, d.global_head_dim, rot_full, &m->rope_full},
+                  {d.rope_base_sliding, d.head_dim, d.head_dim, &m->rope_sliding}};
+    for (int kind = 0; kind < 2; kind++) {
+        Kind& k = kinds[kind];
+        bool used = false;
+        for (uint32_t l = 0; l < d.layers; l++) used |= (m->layer_is_sliding[l] != 0) == (kind == 1);
+        if (!used) continue;
+        if (k.rotary % 2 || k.rotary > k.hd) return IRIS_E_INVALID;
+        if (k.rotary == 0) continue;
+        if (k.hd < 2 || k.hd % 2 || k.base <= 0) return IRIS_E_INVALID;
+        if (*k.table) continue;
+        RT_CHECK(hipMalloc((void**)k.table, (k.rotary / 2) * sizeof(int64_t)));
+        RT_CHECK(iris_rope_ladder_launch(k.base, k.hd, k.rotary / 2, *k.table, m->stream));
+    }
+    const uint32_t shared = d.num_kv_shared_layers;
+    const uint32_t first_shared = d.layers > shared ? d.layers - shared : 0;
+    for (uint32_t l = 0; l < d.layers; l++) {
+        LayerWeights& L = m->layers[l];
+        if (!L.norm_post_attn || !L.norm_post_ffw || !L.norm_post_ple || !L.q_norm || !L.k_norm || !L.ple_gate ||
+            !L.ple_proj)
+            return IRIS_E_STATE;
+        const bool sliding = m->layer_is_sliding[l] != 0;
+        const Kind& k = kinds[sliding ? 1 : 0];
+        L.head_dim = k.hd;
+        L.rotary_dim = k.rotary;
+        L.inv_freq = *k.table;
+        L.window = sliding ? d.sliding_window : 0;
+        L.kv_source = (int32_t)l;
+        if (shared != 0 && l >= first_shared) {
+            for (int32_t c = (int32_t)first_shared - 1; c >= 0; c--)
+                if (m->layer_is_sliding[c] == m->layer_is_sliding[l]) {
+                    L.kv_source = c;
+                    break;
+                }
+        }
+    }
+    return (int)hipStreamSynchronize(m->stream);
+}
+
 int iris_model_finalize(IrisModel* m) {
     if (!m) return IRIS_E_INVALID;
     const IrisModelDesc& d = m->d;
-    if (!m->embed_raw || !m->head || !m->final_norm || !m->inv_freq) return IRIS_E_STATE;
+    const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
+    if (!m->embed_raw || !m->head || !m->final_norm || (!gemma && !m->inv_freq)) return IRIS_E_STATE;
+    if (gemma) RT_CHECK(gemma_finalize(m));
     for (uint32_t l = 0; l < d.layers; l++) {
-        const LayerWeights& L = m->layers[l];
+        LayerWeights& L = m->layers[l];
         if (!L.wqkv || !L.wo || !L.wgu || !L.wdown || !L.norm_attn || !L.norm_ff) return IRIS_E_STATE;
-        if (L.q_rows != d.heads * d.head_dim || L.kv_rows != d.kv_heads * d.head_dim || L.ffn != d.ffn)
+        if (!gemma) {
+            L.head_dim = d.head_dim;
+            L.kv_source = (int32_t)l;
+        }
+        if (L.q_rows != d.heads * L.head_dim || L.kv_rows != d.kv_heads * L.head_dim || (!gemma && L.ffn != d.ffn))
             return IRIS_E_INVALID;
-        if (L.wo->rows != d.hidden || L.wo->cols != L.q_rows || L.wdown->rows != d.hidden || L.wdown->cols != d.ffn)
+        if (L.wo->rows != d.hidden || L.wo->cols != L.q_rows || L.wdown->rows != d.hidden || L.wdown->cols != L.ffn)
             return IRIS_E_INVALID;
+        m->max_head_dim = std::max(m->max_head_dim, L.head_dim);
+        m->max_ffn = std::max(m->max_ffn, L.ffn);
+        m->max_qkv = std::max(m->max_qkv, L.q_rows + 2 * L.kv_rows);
         m->pending[l].clear();
     }
     m->finalized = true;
@@ -224,6 +345,10 @@ uint64_t iris_model_device_bytes(const IrisModel* m) {
         for (const Q8GpuMatrix* w : {L.wqkv, L.wo, L.wgu, L.wdown})
             if (w) b += w->device_bytes;
     if (m->head) b += m->head->device_bytes;
+    if (m->d.family == IRIS_FAMILY_GEMMA_DENSE) {
+        const uint64_t hp = (uint64_t)m->d.hidden * m->d.ple_width * 4;
+        b += (uint64_t)m->layers.size() * 2 * hp + (uint64_t)m->d.layers * hp;  // PLE matrices
+    }
     return b;
 }
 
@@ -234,13 +359,19 @@ void iris_model_free(IrisModel* m) {
         q8gpu_free(L.wo);
         q8gpu_free(L.wgu);
         q8gpu_free(L.wdown);
-        hipFree(L.norm_attn);
-        hipFree(L.norm_ff);
+        for (int32_t* p : {L.norm_attn, L.norm_ff, L.norm_post_attn, L.norm_post_ffw, L.norm_post_ple, L.q_norm,
+                           L.k_norm, L.ple_gate, L.ple_proj})
+            hipFree(p);
     }
     q8gpu_free(m->head);
     hipFree(m->embed_raw);
     hipFree(m->final_norm);
     hipFree(m->inv_freq);
+    hipFree(m->embed_ple);
+    hipFree(m->ple_model_proj);
+    hipFree(m->ple_proj_norm);
+    hipFree(m->rope_sliding);
+    hipFree(m->rope_full);
     if (m->stream) hipStreamDestroy(m->stream);
     delete m;
 }
@@ -249,7 +380,7 @@ void iris_model_free(IrisModel* m) {
 
 // ---------------------------------------------------------------- session
 
-static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
+static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     const uint32_t H = d.hidden;
@@ -345,6 +476,168 @@ static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
     return 0;
 }
 
+// One gemma-dense pass (crates/inference/kernels/src/prefill_range.rs:307-958
+// per layer, the PLE prepare of view_kernels.rs:59-99 first): eleven launches
+// per layer.
+static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    const uint32_t H = d.hidden, P = d.ple_width, LP = d.layers * d.ple_width;
+    hipStream_t st = s->stream;
+    // PLE inputs of every layer from the embedded rows and their ids.
+    I32GemvArgs ig{};
+    ig.w = m->ple_model_proj;
+    ig.rows = LP;
+    ig.cols = H;
+    ig.x = s->x;
+    ig.x_stride = H;
+    ig.out = s->ple_proj;
+    ig.out_stride = LP;
+    RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
+    PleArgs pa{};
+    pa.proj = s->ple_proj;
+    pa.row_stride = LP;
+    pa.ids = s->ids;
+    pa.emb = m->embed_ple;
+    pa.emb_row_bytes = m->embed_ple_row_bytes;
+    pa.ple_width = P;
+    pa.norm_w = m->ple_proj_norm;
+    pa.eps = d.norm_eps;
+    pa.projection_scalar = d.ple_projection_scalar;
+    pa.embedding_scale = d.ple_embedding_scale;
+    pa.input_scale = d.ple_input_scale;
+    pa.out = s->ple_rows;
+    RT_CHECK(iris_ple_prepare_launch(pa, d.layers, rows, st));
+    for (uint32_t l = 0; l < d.layers; l++) {
+        const LayerWeights& L = m->layers[l];
+        const uint32_t hd = L.head_dim, qw = L.q_rows, kvw = L.kv_rows, qkvw = qw + 2 * kvw;
+        // 1. q|k|v = W_qkv rms_norm(x, input_layernorm)  (project_tokens :497-579)
+        GemvArgs g{};
+        g.w = q8_view(L.wqkv);
+        g.x = s->x;
+        g.x_stride = H;
+        g.tokens = rows;
+        g.prologue = PRO_RMSNORM;
+        g.norm_w = L.norm_attn;
+        g.norm_eps = d.norm_eps;
+        g.epilogue = EPI_STORE;
+        g.out = s->qkv;
+        g.out_stride = qkvw;
+        RT_CHECK(iris_gemv_launch(g, st));
+        // 2. per-head norms and RoPE, K/V into the layer's own cache (:607-647)
+        GemmaQkvArgs qa{};
+        qa.qkv = s->qkv;
+        qa.qkv_stride = qkvw;
+        qa.heads = d.heads;
+        qa.kv_heads = d.kv_heads;
+        qa.head_dim = hd;
+        qa.rotary_dim = L.rotary_dim;
+        qa.q_norm = L.q_norm;
+        qa.k_norm = L.k_norm;
+        qa.eps = d.norm_eps;
+        qa.inv_freq = L.inv_freq;
+        qa.d_pos = s->d_pos;
+        qa.q_out = s->q;
+        qa.q_stride = qw;
+        qa.k_cache = s->k_cache[l];
+        qa.k_pos_stride = s->max_positions;
+        qa.v_cache = s->v_cache[l];
+        RT_CHECK(iris_gemma_qkv_finish_launch(qa, rows, st));
+        // 3. attention over the window of the source layer's cache (:692-845)
+        AttnArgs a{};
+        a.q = s->q;
+        a.q_stride = qw;
+        a.k_cache = s->k_cache[L.kv_source];
+        a.k_pos_stride = s->max_positions;
+        a.v_cache = s->v_cache[L.kv_source];
+        a.kv_stride = kvw;
+        a.ctx = s->ctx;
+        a.ctx_stride = qw;
+        a.d_pos = s->d_pos;
+        a.heads = d.heads;
+        a.kv_heads = d.kv_heads;
+        a.head_dim = hd;
+        a.scaled = 0;
+        a.window = L.window;
+        a.scores = s->attn_scores;
+        a.chunk_max = s->attn_chunk_max;
+        a.chunk_acc = s->attn_chunk_acc;
+        a.chunk_wsum = s->attn_chunk_wsum;
+        a.max_weight = s->attn_max_weight;
+        RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
+        // 4. attended = rms_norm(W_o ctx, post_attention) + x  (:879-892)
+        g = GemvArgs{};
+        g.w = q8_view(L.wo);
+        g.x = s->ctx;
+        g.x_stride = qw;
+        g.tokens = rows;
+        g.epilogue = EPI_STORE;
+        g.out = s->tmp;
+        g.out_stride = H;
+        RT_CHECK(iris_gemv_launch(g, st));
+        RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_attn, d.norm_eps, s->x, H, 0, s->attended, H, H,
+                                           rows, st));
+        // 5. gated = mul(gelu(W_gate f), W_up f), f = rms_norm(attended, pre_ffw)  (:894-913)
+        g = GemvArgs{};
+        g.w = q8_view(L.wgu);
+        g.x = s->attended;
+        g.x_stride = H;
+        g.tokens = rows;
+        g.prologue = PRO_RMSNORM;
+        g.norm_w = L.norm_ff;
+        g.norm_eps = d.norm_eps;
+        g.epilogue = EPI_GEGLU;
+        g.out = s->gated;
+        g.out_stride = L.ffn;
+        RT_CHECK(iris_gemv_launch(g, st));
+        // 6. attended = rms_norm(W_down gated, post_ffw) + attended  (finish_mlp :915-929)
+        g = GemvArgs{};
+        g.w = q8_view(L.wdown);
+        g.x = s->gated;
+        g.x_stride = L.ffn;
+        g.tokens = rows;
+        g.epilogue = EPI_STORE;
+        g.out = s->tmp;
+        g.out_stride = H;
+        RT_CHECK(iris_gemv_launch(g, st));
+        RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ffw, d.norm_eps, s->attended, H, 0, s->attended, H,
+                                           H, rows, st));
+        // 7. PLE block: g = mul(gelu(gate attended), ple); x = rms_norm(proj g) + attended,
+        //    times the layer scalar (:931-958)
+        ig = I32GemvArgs{};
+        ig.w = L.ple_gate;
+        ig.rows = P;
+        ig.cols = H;
+        ig.x = s->attended;
+        ig.x_stride = H;
+        ig.out = s->ple_gated;
+        ig.out_stride = P;
+        ig.aux = s->ple_rows + (size_t)l * P;
+        ig.aux_stride = LP;
+        RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
+        ig = I32GemvArgs{};
+        ig.w = L.ple_proj;
+        ig.rows = H;
+        ig.cols = P;
+        ig.x = s->ple_gated;
+        ig.x_stride = P;
+        ig.out = s->tmp;
+        ig.out_stride = H;
+        RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
+        RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ple, d.norm_eps, s->attended, H, L.layer_scalar,
+                                           s->x, H, H, rows, st));
+        if (layer_rows_out)
+            RT_CHECK(hipMemcpyAsync(layer_rows_out + (size_t)l * rows * H, s->x, (size_t)rows * H * 4,
+                                    hipMemcpyDeviceToHost, st));
+    }
+    return 0;
+}
+
+static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
+    if (s->model->d.family == IRIS_FAMILY_GEMMA_DENSE) return gemma_pass(s, rows, layer_rows_out);
+    return mistral_pass(s, rows, layer_rows_out);
+}
+
 static int session_head_select(IrisSession* s, uint32_t rows) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
@@ -370,6 +663,7 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     g.hidden = d.hidden;
     g.embed_scale = m->embed_scale;
     g.x_next = s->x;
+    g.ids_next = m->d.family == IRIS_FAMILY_GEMMA_DENSE ? s->ids : nullptr;
     g.sel_partial = s->sel_partial;
     RT_CHECK(iris_gemv_launch(g, s->stream));
     return iris_select_launch(g, s->stream);
@@ -382,7 +676,8 @@ static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t 
     RT_CHECK(hipMemsetAsync(s->d_pos, 0, sizeof(int32_t), s->stream));
     RT_CHECK(hipMemsetAsync(s->d_step, 0, sizeof(int32_t), s->stream));
     RT_CHECK(hipMemcpyAsync(s->ids, ids, (size_t)count * 4, hipMemcpyHostToDevice, s->stream));
-    return iris_embed_rows_launch(s->ids, count, m->embed_raw, m->embed_row_bytes, m->d.hidden, 0, s->x, s->stream);
+    return iris_embed_rows_launch(s->ids, count, m->embed_raw, m->embed_row_bytes, m->d.hidden, m->embed_scale, s->x,
+                                  s->stream);
 }
 
 // Captures the decode pass (one row, head, select) as a graph. Each
@@ -428,11 +723,12 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     s->model = m;
     s->max_positions = max_positions;
     s->max_rows = max_rows;
-    const size_t qw = (size_t)d.heads * d.head_dim, kvw = (size_t)d.kv_heads * d.head_dim;
+    const size_t qw = (size_t)d.heads * m->max_head_dim;
     hipError_t st = hipStreamCreate(&s->stream);
     s->k_cache.assign(d.layers, nullptr);
     s->v_cache.assign(d.layers, nullptr);
     for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++) {
+        const size_t kvw = m->layers[l].kv_rows;
         st = hipMalloc((void**)&s->k_cache[l], (size_t)max_positions * kvw * 4);
         if (st == hipSuccess) st = hipMalloc((void**)&s->v_cache[l], (size_t)max_positions * kvw * 4);
     }
@@ -443,7 +739,15 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->attended, (size_t)max_rows * d.hidden);
     alloc(&s->q, (size_t)max_rows * qw);
     alloc(&s->ctx, (size_t)max_rows * qw);
-    alloc(&s->gated, (size_t)max_rows * d.ffn);
+    alloc(&s->gated, (size_t)max_rows * m->max_ffn);
+    if (d.family == IRIS_FAMILY_GEMMA_DENSE) {
+        const size_t lp = (size_t)d.layers * d.ple_width;
+        alloc(&s->qkv, (size_t)max_rows * m->max_qkv);
+        alloc(&s->tmp, (size_t)max_rows * d.hidden);
+        alloc(&s->ple_proj, (size_t)max_rows * lp);
+        alloc(&s->ple_rows, (size_t)max_rows * lp);
+        alloc(&s->ple_gated, (size_t)max_rows * d.ple_width);
+    }
     alloc(&s->logits, d.vocab);
     alloc(&s->ids, max_rows);
     alloc(&s->tokens, max_positions + 1);
@@ -454,7 +758,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     if (st == hipSuccess) st = hipMalloc((void**)&s->attn_scores, heads * ATTN_MAX_KEYS * sizeof(int32_t));
     if (st == hipSuccess) st = hipMalloc((void**)&s->attn_chunk_max, heads * ATTN_MAX_CHUNKS * sizeof(uint64_t));
     if (st == hipSuccess)
-        st = hipMalloc((void**)&s->attn_chunk_acc, heads * ATTN_MAX_CHUNKS * d.head_dim * sizeof(int64_t));
+        st = hipMalloc((void**)&s->attn_chunk_acc, heads * ATTN_MAX_CHUNKS * m->max_head_dim * sizeof(int64_t));
     if (st == hipSuccess) st = hipMalloc((void**)&s->attn_chunk_wsum, heads * ATTN_MAX_CHUNKS * sizeof(int32_t));
     if (st == hipSuccess) st = hipMalloc((void**)&s->attn_max_weight, heads * sizeof(int32_t));
     if (st != hipSuccess) {
@@ -471,7 +775,7 @@ void iris_session_free(IrisSession* s) {
     for (auto p : s->k_cache) hipFree(p);
     for (auto p : s->v_cache) hipFree(p);
     for (int32_t* p : {s->x, s->attended, s->q, s->ctx, s->gated, s->logits, s->ids, s->tokens, s->d_pos, s->d_step,
-                       s->logits_keep})
+                       s->logits_keep, s->qkv, s->tmp, s->ple_proj, s->ple_rows, s->ple_gated})
         hipFree(p);
     hipFree(s->sel_partial);
     hipFree(s->attn_scores);

@@ -17,9 +17,22 @@ struct LayerWeights {
     Q8GpuMatrix* wo = nullptr;
     Q8GpuMatrix* wgu = nullptr;    // gate/up rows interleaved
     Q8GpuMatrix* wdown = nullptr;
-    int32_t* norm_attn = nullptr;
-    int32_t* norm_ff = nullptr;
+    int32_t* norm_attn = nullptr;  // input_layernorm
+    int32_t* norm_ff = nullptr;    // pre_feedforward_layernorm
     uint32_t q_rows = 0, kv_rows = 0, ffn = 0;
+    // gemma-dense only
+    int32_t* norm_post_attn = nullptr;
+    int32_t* norm_post_ffw = nullptr;
+    int32_t* norm_post_ple = nullptr;  // post_per_layer_input_norm
+    int32_t* q_norm = nullptr;
+    int32_t* k_norm = nullptr;
+    int32_t* ple_gate = nullptr;       // per_layer_input_gate, Q16.16 [ple][hidden]
+    int32_t* ple_proj = nullptr;       // per_layer_projection, Q16.16 [hidden][ple]
+    int32_t layer_scalar = 0;          // 0 = absent
+    // derived at finalize (model.rs:817-877)
+    uint32_t head_dim = 0, rotary_dim = 0, window = 0;
+    int32_t kv_source = -1;            // the layer whose cache attention reads
+    const int64_t* inv_freq = nullptr; // [rotary_dim / 2]
 };
 
 struct IrisModel {
@@ -35,6 +48,14 @@ struct IrisModel {
     int64_t* inv_freq = nullptr;
     int32_t head_softcap = 0;   // 0 = uncapped (mistral-dense)
     int32_t embed_scale = 0;    // 0 = unscaled (mistral-dense)
+    // gemma-dense only
+    uint8_t* embed_ple = nullptr;        // embed_tokens_per_layer, reference Q8_0 rows
+    uint32_t embed_ple_row_bytes = 0;
+    int32_t* ple_model_proj = nullptr;   // per_layer_model_projection, Q16.16 [layers*ple][hidden]
+    int32_t* ple_proj_norm = nullptr;    // per_layer_projection_norm [ple]
+    int64_t* rope_sliding = nullptr;     // frequency ladders of the two layer kinds
+    int64_t* rope_full = nullptr;
+    uint32_t max_head_dim = 0, max_ffn = 0, max_qkv = 0;
     hipStream_t stream = nullptr;
     bool finalized = false;
 };
@@ -45,6 +66,9 @@ struct IrisSession {
     hipStream_t stream = nullptr;
     std::vector<int32_t*> k_cache, v_cache;  // per layer [position][kv_heads*head_dim]
     int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;
+    // gemma-dense only: raw q|k|v rows, a product's rows before their norm,
+    // the PLE projections and inputs of every layer, the PLE gate output
+    int32_t *qkv = nullptr, *tmp = nullptr, *ple_proj = nullptr, *ple_rows = nullptr, *ple_gated = nullptr;
     int32_t *logits = nullptr, *ids = nullptr, *tokens = nullptr;
     int32_t *d_pos = nullptr, *d_step = nullptr;
     int32_t* logits_keep = nullptr;

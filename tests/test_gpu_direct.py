@@ -1,8 +1,8 @@
 """GPU parity of the whole token loop against the oracle, through the C ABI:
 every selected token and every logit the selection was made from, with and
-without graph replay, on a small mistral-dense model, on the reference's
-parity-mistral bundle cases (EOS included), and at Mistral-7B shape; plus
-the teacher-forced per-layer pass (rows and per-layer SHA-256)."""
+without graph replay, for both families: small models, the reference's
+parity bundle cases (EOS included), and the Mistral-7B and Gemma-2B shapes;
+plus the teacher-forced per-layer pass (rows and per-layer SHA-256)."""
 import hashlib
 
 import numpy as np
@@ -81,6 +81,70 @@ def test_mistral_7b_shape_generation_matches_oracle():
     s = Session(dm, 64, 8)
     got = s.generate(prompt, 3, keep_logits=True)
     print("mistral-7b shape: oracle", flush=True)
+    want_tokens, want_logits = _oracle_generate(m, prompt, 3, 64)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+
+
+# ---------------------------------------------------------------- gemma-dense
+
+@pytest.mark.parametrize("case", [0, 1, 2])
+def test_parity_gemma_bundle_cases(case):
+    # Sliding layers (window 16) alternating with full ones, two KV-shared
+    # layers, partial rotary on the full layers, softcap 1.0, untied head:
+    # the cases run inside, across and past the window.
+    g = golden("parity_bundles.json")["bundles"]["parity-gemma"]
+    c = g["cases"][case]
+    m = model_mod.from_detwgt(synth.parity_gemma_detwgt(), "gemma-dense", synth.parity_gemma_shape(),
+                              eos_token_ids=g["eos_token_ids"])
+    print(f"parity-gemma case {c['name']}", flush=True)
+    dm = DeviceModel(m)
+    s = Session(dm, 128, 64)
+    got = s.generate(c["input_token_ids"], c["tokens"], keep_logits=True)
+    want_tokens, want_logits = _oracle_generate(m, c["input_token_ids"], c["tokens"], 128)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+
+
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_tiny_gemma_generation_matches_oracle(use_graph):
+    # 2 layers, hidden 256, 4 heads of 64 over 1 KV head, GeGLU 1024, vocab
+    # 4096, PLE 64, softcap 30: a 16-token prompt and 32 greedy selections.
+    m = synth.tiny_gemma()
+    prompt = synth.token_ids(11, 16, 4096)
+    print(f"tiny gemma, graph={use_graph}", flush=True)
+    dm = DeviceModel(m)
+    s = Session(dm, 64, 16)
+    got = s.generate(prompt, 32, keep_logits=True, use_graph=use_graph)
+    want_tokens, want_logits = _oracle_generate(m, prompt, 32, 64)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+
+
+def test_gemma_teacher_forced_layer_pass_matches_oracle():
+    m = model_mod.from_detwgt(synth.parity_gemma_detwgt(), "gemma-dense", synth.parity_gemma_shape())
+    ids = synth.token_ids(6, 40, m.vocab)
+    dm = DeviceModel(m)
+    s = Session(dm, 64, 64)
+    rows, hashes = s.layer_pass(ids)
+    r = cpu.OracleRun(m, 64)
+    _, layers = r.pass_rows(list(ids), 0, keep_layers=True)
+    for layer in range(m.num_layers):
+        assert np.array_equal(rows[layer], layers[layer]), layer
+        assert hashes[layer] == hashlib.sha256(layers[layer].astype("<i4").tobytes()).hexdigest()
+
+
+def test_gemma_2b_shape_generation_matches_oracle():
+    # The Gemma-2B configuration's shape (18 layers, hidden 2048, 8 heads of
+    # 256 over 1 KV head, GeGLU 16384, vocab 256000, PLE 256, softcap 30):
+    # a short prompt and three selections, every logit against the oracle.
+    m = synth.gemma_2b()
+    prompt = synth.token_ids(8, 4, m.vocab)
+    print("gemma-2b shape: uploading", flush=True)
+    dm = DeviceModel(m)
+    s = Session(dm, 64, 8)
+    got = s.generate(prompt, 3, keep_logits=True)
+    print("gemma-2b shape: oracle", flush=True)
     want_tokens, want_logits = _oracle_generate(m, prompt, 3, 64)
     assert got.token_ids == want_tokens
     assert np.array_equal(got.logits, np.stack(want_logits))
