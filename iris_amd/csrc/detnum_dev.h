@@ -165,7 +165,13 @@ __device__ inline int32_t inv_sqrt_acc(int64_t x) {
     const uint32_t max_bits = (uint32_t)INT32_MAX;
     auto prod = [&](uint32_t c) -> u128 { return (u128)((uint64_t)c * (uint64_t)c) * divisor; };
     if (prod(max_bits) <= target) return INT32_MAX;
-    double est = floor(sqrt(18446744073709551616.0 / (double)(uint64_t)x));
+    // Estimate 2^32 / sqrt(x) from the hardware reciprocal square root and
+    // one Newton step; the exact search below does not depend on its quality.
+    const double xd = (double)(uint64_t)x;
+    double y = __builtin_amdgcn_rsq(xd);
+    y = y * (1.5 - 0.5 * xd * y * y);
+    double est = floor(4294967296.0 * y);
+    if (!(est >= 0.0)) est = 0.0;
     uint32_t low = est >= (double)max_bits ? max_bits : (uint32_t)est;
     while (low < max_bits && prod(low + 1) <= target) low++;
     while (low > 0 && prod(low) > target) low--;
@@ -181,9 +187,36 @@ __device__ inline int32_t inv_sqrt_acc(int64_t x) {
     return (int32_t)r;
 }
 
+// ops.rs:81-88 div_acc_by_u32 for a non-negative dividend: the floor
+// quotient from a refined hardware reciprocal, made exact by integer
+// correction, then rounded half to even. (The generic 64-bit division is a
+// long software sequence; this is the hot case, the mean of a sum of squares.)
+__device__ __forceinline__ int64_t div_nonneg_by_u32(int64_t value, uint32_t n) {
+    const uint64_t u = (uint64_t)value;
+    const double nd = (double)n;
+    double r = __builtin_amdgcn_rcp(nd);
+    r = r * (2.0 - nd * r);
+    r = r * (2.0 - nd * r);
+    uint64_t q = (uint64_t)((double)u * r);
+    int64_t rem = (int64_t)(u - q * (uint64_t)n);
+    q = (uint64_t)((int64_t)q + (int64_t)((double)rem * r));
+    rem = (int64_t)(u - q * (uint64_t)n);
+    while (rem < 0) {
+        q--;
+        rem += n;
+    }
+    while (rem >= (int64_t)n) {
+        q++;
+        rem -= n;
+    }
+    const uint64_t twice = (uint64_t)rem * 2;
+    if (twice > n || (twice == n && (q & 1))) q++;
+    return (int64_t)q;
+}
+
 // ops.rs:409-428 after the (order-free, saturating) sum of squares.
 __device__ __forceinline__ int32_t rms_scale_from_sum(int64_t sum_squares, uint32_t n, int64_t eps) {
-    int64_t mean = div_acc_by_u32(sum_squares, n);
+    int64_t mean = div_nonneg_by_u32(sum_squares, n);
     return inv_sqrt_acc(acc_add_sat(mean, eps));
 }
 

@@ -37,6 +37,11 @@ __device__ __forceinline__ int64_t wave_sum_sat_nonneg(int64_t v) {
     return v;
 }
 
+__device__ __forceinline__ int wave_max_int(int v) {
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off));
+    return v;
+}
+
 // Sum of the four kgroups (lanes r, r+16, r+32, r+48) of a wave.
 __device__ __forceinline__ dn::i128 kgroup_sum(dn::i128 v) {
     for (int off = 16; off <= 32; off <<= 1) {
@@ -248,11 +253,152 @@ __device__ __forceinline__ int stage_planes(const int32_t* x, const int32_t* nor
     return need;
 }
 
+// Digit planes of the four values at dword index i (after the optional
+// norm: mul_sat(mul_sat(v, scale), w)); returns the digits the largest needs.
+__device__ __forceinline__ int stage_int4(int4 v, bool norm, int4 nw, int32_t scale, uint32_t i, uint32_t* planes,
+                                          uint32_t pw) {
+    if (norm) {
+        v.x = dn::mul_sat(dn::mul_sat(v.x, scale), nw.x);
+        v.y = dn::mul_sat(dn::mul_sat(v.y, scale), nw.y);
+        v.z = dn::mul_sat(dn::mul_sat(v.z, scale), nw.z);
+        v.w = dn::mul_sat(dn::mul_sat(v.w, scale), nw.w);
+    }
+    const uint64_t d0 = digits5(v.x), d1 = digits5(v.y), d2 = digits5(v.z), d3 = digits5(v.w);
+    const int need = max(max(limbs_needed(d0), limbs_needed(d1)), max(limbs_needed(d2), limbs_needed(d3)));
+#pragma unroll
+    for (int l = 0; l < MAX_LIMBS; l++) {
+        const int sh = 8 * l;
+        planes[l * pw + i] = (uint32_t)((d0 >> sh) & 0xff) | ((uint32_t)((d1 >> sh) & 0xff) << 8) |
+                             ((uint32_t)((d2 >> sh) & 0xff) << 16) | ((uint32_t)((d3 >> sh) & 0xff) << 24);
+    }
+    return need;
+}
+
+__device__ __forceinline__ int64_t sumsq4(int64_t s, int4 v) {
+    s = dn::acc_add_sat(s, (int64_t)v.x * v.x);
+    s = dn::acc_add_sat(s, (int64_t)v.y * v.y);
+    s = dn::acc_add_sat(s, (int64_t)v.z * v.z);
+    return dn::acc_add_sat(s, (int64_t)v.w * v.w);
+}
+
+constexpr uint32_t XROUND = 4;  // int4 loads a thread has in flight per staging round
+
+// The persistent kernel's prologue: the row's rms_norm scale when asked
+// (sum of squares: saturating, non-negative terms, so order-free) and every
+// digit plane of the row in LDS. A thread issues XROUND 16-byte loads (with
+// their norm weights) before it uses any of them; a row of at most
+// XROUND * GEMV_THREADS dwords is read once and kept in registers between
+// the two steps. Returns the digits the row needs.
+__device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes, int64_t* ssq,
+                         int32_t* s_scale, uint32_t tid) {
+    const uint32_t lane = tid & 63, wave = tid >> 6;
+    const bool norm = a.prologue == PRO_RMSNORM;
+    const int4* x4 = (const int4*)x;
+    // Without a norm the weight loads read the row again (unused): every
+    // load is unconditional and issued in program order.
+    const int4* n4 = norm ? (const int4*)a.norm_w : x4;
+    // Out-of-range slots load the row's last dword (always valid) and are
+    // dropped afterwards, so no load waits on a branch.
+    auto load_round = [&](uint32_t i0, int4 (&v)[XROUND], int4 (&nw)[XROUND]) {
+#pragma unroll
+        for (uint32_t u = 0; u < XROUND; u++) v[u] = x4[min(i0 + u * GEMV_THREADS + tid, pw - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < XROUND; u++) nw[u] = n4[min(i0 + u * GEMV_THREADS + tid, pw - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto round_sumsq = [&](uint32_t i0, const int4 (&v)[XROUND], int64_t s) {
+#pragma unroll
+        for (uint32_t u = 0; u < XROUND; u++) {
+            const bool ok = i0 + u * GEMV_THREADS + tid < pw;
+            const int4 m = make_int4(ok ? v[u].x : 0, ok ? v[u].y : 0, ok ? v[u].z : 0, ok ? v[u].w : 0);
+            s = sumsq4(s, m);
+        }
+        return s;
+    };
+    auto round_stage = [&](uint32_t i0, const int4 (&v)[XROUND], const int4 (&nw)[XROUND], int32_t scale, int need) {
+#pragma unroll
+        for (uint32_t u = 0; u < XROUND; u++) {
+            const uint32_t i = i0 + u * GEMV_THREADS + tid;
+            if (i < pw) need = max(need, stage_int4(v[u], norm, nw[u], scale, i, planes, pw));
+        }
+        return need;
+    };
+    auto finish_scale = [&](int64_t s) -> int32_t {
+        s = wave_sum_sat_nonneg(s);
+        if (lane == 0) ssq[wave] = s;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t t = 0;
+            for (int i = 0; i < GEMV_WAVES; i++) t = dn::acc_add_sat(t, ssq[i]);
+            *s_scale = dn::rms_scale_from_sum(t, pw * 4, a.norm_eps);
+        }
+        __syncthreads();
+        return *s_scale;
+    };
+    int4 v[XROUND], nw[XROUND];
+    if (pw <= XROUND * GEMV_THREADS) {
+        load_round(0, v, nw);
+        const int32_t scale = norm ? finish_scale(round_sumsq(0, v, 0)) : 0;
+        return round_stage(0, v, nw, scale, 1);
+    }
+    int32_t scale = 0;
+    if (norm) {
+        int64_t s = 0;
+        for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * GEMV_THREADS) {
+            load_round(i0, v, nw);
+            s = round_sumsq(i0, v, s);
+        }
+        scale = finish_scale(s);
+    }
+    int need = 1;
+    for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * GEMV_THREADS) {
+        load_round(i0, v, nw);
+        need = round_stage(i0, v, nw, scale, need);
+    }
+    return need;
+}
+
 // One block's contribution to the lane's accumulator.
 template <int L, int MODE>
 __device__ __forceinline__ void accumulate_block(const uint4 q0, const uint4 q1, uint32_t sbits, int64_t sc64,
                                                  const uint32_t* lb, uint32_t pw, int64_t& acc64, dn::i128& acc128) {
     const int64_t bs = block_sum_pw<L>(q0, q1, lb, pw);
+    if constexpr (MODE == Q8_SCALE_ROW) {
+        acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
+    } else if constexpr (MODE == Q8_SCALE_F16) {
+        const uint32_t e = (sbits >> 10) & 0x1f;
+        const int64_t m = (int64_t)(sbits & 0x3ff) | (e ? 1024 : 0);
+        int64_t p = bs * m;  // < 2^55
+        if (sbits & 0x8000) p = -p;
+        acc128 += (dn::i128)p << (e ? e - 1 : 0);
+    } else {
+        acc128 += (dn::i128)bs * (dn::i128)sc64;
+    }
+}
+
+// accumulate_block with the digit count L a runtime value (uniform over the
+// workgroup, so the plane loop's branches are scalar).
+template <int MODE>
+__device__ __forceinline__ void accumulate_block_rt(const uint4 q0, const uint4 q1, uint32_t sbits, int64_t sc64,
+                                                    const uint32_t* lb, uint32_t pw, int L, int64_t& acc64,
+                                                    dn::i128& acc128) {
+    int64_t bs = 0;
+#pragma unroll
+    for (int l = 0; l < MAX_LIMBS; l++) {
+        if (l < L) {
+            const uint32_t* p = lb + l * pw;
+            int s = 0;
+            s = __builtin_amdgcn_sdot4((int)q0.x, (int)p[0], s, false);
+            s = __builtin_amdgcn_sdot4((int)q0.y, (int)p[1], s, false);
+            s = __builtin_amdgcn_sdot4((int)q0.z, (int)p[2], s, false);
+            s = __builtin_amdgcn_sdot4((int)q0.w, (int)p[3], s, false);
+            s = __builtin_amdgcn_sdot4((int)q1.x, (int)p[4], s, false);
+            s = __builtin_amdgcn_sdot4((int)q1.y, (int)p[5], s, false);
+            s = __builtin_amdgcn_sdot4((int)q1.z, (int)p[6], s, false);
+            s = __builtin_amdgcn_sdot4((int)q1.w, (int)p[7], s, false);
+            bs += (int64_t)s << (8 * l);
+        }
+    }
     if constexpr (MODE == Q8_SCALE_ROW) {
         acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
     } else if constexpr (MODE == Q8_SCALE_F16) {
@@ -298,23 +444,25 @@ __device__ __forceinline__ uint32_t lane_block_count(uint32_t nb, uint32_t slot,
 }
 
 // All of one tile's blocks this lane owns (slot, slot + nslots, ...), against
-// digit planes covering the whole row (plane stride pw dwords). Loads run one
-// batch ahead of the arithmetic.
-template <int L, int MODE>
+// L digit planes covering the whole row (plane stride pw dwords). Loads run
+// one batch ahead of the arithmetic; the first batch is fetched here unless
+// the caller has already issued it into `cur`.
+template <int MODE>
 __device__ __forceinline__ void tile_blocks(const Q8View& w, uint32_t tile, uint32_t slot, uint32_t nslots, uint32_t r,
-                                            const uint32_t* planes, uint32_t pw, int64_t& acc64, dn::i128& acc128) {
+                                            const uint32_t* planes, uint32_t pw, int L, int64_t& acc64,
+                                            dn::i128& acc128, BlockBatch& cur, bool prefetched) {
     const uint32_t cnt = lane_block_count(w.nb, slot, nslots);
     if (cnt == 0) return;
     const uint32_t last = slot + (cnt - 1) * nslots;
-    BlockBatch cur, nxt;
-    fetch_batch<MODE>(w, tile, slot, nslots, last, r, 0, cur);
+    if (!prefetched) fetch_batch<MODE>(w, tile, slot, nslots, last, r, 0, cur);
+    BlockBatch nxt;
     for (uint32_t k0 = 0; k0 < cnt; k0 += BATCH) {
         if (k0 + BATCH < cnt) fetch_batch<MODE>(w, tile, slot, nslots, last, r, k0 + BATCH, nxt);
 #pragma unroll
         for (int u = 0; u < BATCH; u++) {
             if (k0 + u < cnt) {
                 const uint32_t b = slot + (k0 + u) * nslots;
-                accumulate_block<L, MODE>(cur.q[u][0], cur.q[u][1], cur.s[u], cur.w[u], planes + b * 8, pw, acc64,
+                accumulate_block_rt<MODE>(cur.q[u][0], cur.q[u][1], cur.s[u], cur.w[u], planes + b * 8, pw, L, acc64,
                                           acc128);
             }
         }
@@ -384,7 +532,8 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
                                         ((uint32_t)((d3 >> sh) & 0xff) << 24);
             }
         }
-        atomicMax(&s_limbs, need);
+        need = wave_max_int(need);  // one LDS atomic per wave, not per lane
+        if (lane == 0) atomicMax(&s_limbs, need);
         __syncthreads();
         switch (s_limbs) {
             case 1: chunk_blocks<1, MODE>(w, tile, cb0, cb1, slot, r, lds, acc64, acc128); break;
@@ -430,28 +579,25 @@ __global__ __launch_bounds__(GEMV_THREADS, 4) void q8_gemv_persistent(const Gemv
     const uint32_t part = wave % split;
     const uint32_t slot = part * 4 + g, nslots = split * 4;
 
-    // Once per workgroup: the norm scale and every digit plane of the row.
-    int32_t scale = 0;
-    if (a.prologue == PRO_RMSNORM) {
-        int64_t s = 0;
-        for (uint32_t k = tid; k < K; k += GEMV_THREADS) s = dn::acc_add_sat(s, (int64_t)x[k] * x[k]);
-        s = wave_sum_sat_nonneg(s);
-        if (lane == 0) ssq[wave] = s;
-        if (tid == 0) s_limbs = 1;
-        __syncthreads();
-        if (tid == 0) {
-            int64_t t = 0;
-            for (int i = 0; i < GEMV_WAVES; i++) t = dn::acc_add_sat(t, ssq[i]);
-            s_scale = dn::rms_scale_from_sum(t, K, a.norm_eps);
+    // The first batch of this wave's first tile goes out before the row is
+    // staged (the weights do not depend on it), so the two latencies overlap.
+    BlockBatch cur;
+    bool prefetched = false;
+    {
+        const uint32_t tile0 = blockIdx.x * per_group + wave / split;
+        const uint32_t cnt = lane_block_count(w.nb, slot, nslots);
+        if (blockIdx.x < groups && tile0 < w.tiles && cnt != 0) {
+            fetch_batch<MODE>(w, tile0, slot, nslots, slot + (cnt - 1) * nslots, r, 0, cur);
+            prefetched = true;
         }
-        __syncthreads();
-        scale = s_scale;
-    } else {
-        if (tid == 0) s_limbs = 1;
-        __syncthreads();
     }
-    const int need = stage_planes(x, a.prologue == PRO_RMSNORM ? a.norm_w : nullptr, scale, 0, pw, planes, pw, tid);
-    atomicMax(&s_limbs, need);
+
+    // Once per workgroup: the norm scale and every digit plane of the row.
+    if (tid == 0) s_limbs = 1;
+    __syncthreads();
+    const int need = stage_row(a, x, pw, planes, ssq, &s_scale, tid);
+    const int wave_need = wave_max_int(need);  // one LDS atomic per wave, not per lane
+    if (lane == 0) atomicMax(&s_limbs, wave_need);
     __syncthreads();
     const int limbs = s_limbs;
 
@@ -459,15 +605,8 @@ __global__ __launch_bounds__(GEMV_THREADS, 4) void q8_gemv_persistent(const Gemv
         const uint32_t tile = grp * per_group + wave / split;
         int64_t acc64 = 0;
         dn::i128 acc128 = 0;
-        if (tile < w.tiles) {
-            switch (limbs) {
-                case 1: tile_blocks<1, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
-                case 2: tile_blocks<2, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
-                case 3: tile_blocks<3, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
-                case 4: tile_blocks<4, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
-                default: tile_blocks<5, MODE>(w, tile, slot, nslots, r, planes, pw, acc64, acc128); break;
-            }
-        }
+        if (tile < w.tiles) tile_blocks<MODE>(w, tile, slot, nslots, r, planes, pw, limbs, acc64, acc128, cur, prefetched);
+        prefetched = false;
         dn::i128 total = MODE == Q8_SCALE_ROW ? (dn::i128)acc64 : acc128;
         total = kgroup_sum(total);
         if (split == 1) {
