@@ -289,6 +289,7 @@ constexpr uint32_t XROUND = 4;  // int4 loads a thread has in flight per staging
 // their norm weights) before it uses any of them; a row of at most
 // XROUND * GEMV_THREADS dwords is read once and kept in registers between
 // the two steps. Returns the digits the row needs.
+template <int NT>
 __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes, int64_t* ssq,
                          int32_t* s_scale, uint32_t tid) {
     const uint32_t lane = tid & 63, wave = tid >> 6;
@@ -301,15 +302,15 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
     // dropped afterwards, so no load waits on a branch.
     auto load_round = [&](uint32_t i0, int4 (&v)[XROUND], int4 (&nw)[XROUND]) {
 #pragma unroll
-        for (uint32_t u = 0; u < XROUND; u++) v[u] = x4[min(i0 + u * GEMV_THREADS + tid, pw - 1)];
+        for (uint32_t u = 0; u < XROUND; u++) v[u] = x4[min(i0 + u * NT + tid, pw - 1)];
 #pragma unroll
-        for (uint32_t u = 0; u < XROUND; u++) nw[u] = n4[min(i0 + u * GEMV_THREADS + tid, pw - 1)];
+        for (uint32_t u = 0; u < XROUND; u++) nw[u] = n4[min(i0 + u * NT + tid, pw - 1)];
         __builtin_amdgcn_sched_barrier(0);
     };
     auto round_sumsq = [&](uint32_t i0, const int4 (&v)[XROUND], int64_t s) {
 #pragma unroll
         for (uint32_t u = 0; u < XROUND; u++) {
-            const bool ok = i0 + u * GEMV_THREADS + tid < pw;
+            const bool ok = i0 + u * NT + tid < pw;
             const int4 m = make_int4(ok ? v[u].x : 0, ok ? v[u].y : 0, ok ? v[u].z : 0, ok ? v[u].w : 0);
             s = sumsq4(s, m);
         }
@@ -318,7 +319,7 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
     auto round_stage = [&](uint32_t i0, const int4 (&v)[XROUND], const int4 (&nw)[XROUND], int32_t scale, int need) {
 #pragma unroll
         for (uint32_t u = 0; u < XROUND; u++) {
-            const uint32_t i = i0 + u * GEMV_THREADS + tid;
+            const uint32_t i = i0 + u * NT + tid;
             if (i < pw) need = max(need, stage_int4(v[u], norm, nw[u], scale, i, planes, pw));
         }
         return need;
@@ -329,14 +330,14 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
         __syncthreads();
         if (tid == 0) {
             int64_t t = 0;
-            for (int i = 0; i < GEMV_WAVES; i++) t = dn::acc_add_sat(t, ssq[i]);
+            for (int i = 0; i < NT / 64; i++) t = dn::acc_add_sat(t, ssq[i]);
             *s_scale = dn::rms_scale_from_sum(t, pw * 4, a.norm_eps);
         }
         __syncthreads();
         return *s_scale;
     };
     int4 v[XROUND], nw[XROUND];
-    if (pw <= XROUND * GEMV_THREADS) {
+    if (pw <= XROUND * NT) {
         load_round(0, v, nw);
         const int32_t scale = norm ? finish_scale(round_sumsq(0, v, 0)) : 0;
         return round_stage(0, v, nw, scale, 1);
@@ -344,14 +345,14 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
     int32_t scale = 0;
     if (norm) {
         int64_t s = 0;
-        for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * GEMV_THREADS) {
+        for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * NT) {
             load_round(i0, v, nw);
             s = round_sumsq(i0, v, s);
         }
         scale = finish_scale(s);
     }
     int need = 1;
-    for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * GEMV_THREADS) {
+    for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * NT) {
         load_round(i0, v, nw);
         need = round_stage(i0, v, nw, scale, need);
     }
@@ -557,11 +558,14 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
     finish_tile<MODE>(a, tile, token, t, lane);
 }
 
-template <int MODE>
-__global__ __launch_bounds__(GEMV_THREADS, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split) {
+// W waves per workgroup: 8 (two workgroups per CU) for matrices with many
+// tiles, 16 (one per CU, the same 16 waves) when a matrix has at most one
+// tile per CU, so that its few tiles still keep every wave slot busy.
+template <int MODE, int W>
+__global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split) {
     extern __shared__ uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
-    __shared__ dn::i128 red[GEMV_WAVES][Q8_TILE_ROWS];
-    __shared__ int64_t ssq[GEMV_WAVES];
+    __shared__ dn::i128 red[W][Q8_TILE_ROWS];
+    __shared__ int64_t ssq[W];
     __shared__ int32_t s_scale;
     __shared__ int s_limbs;
 
@@ -573,8 +577,8 @@ __global__ __launch_bounds__(GEMV_THREADS, 4) void q8_gemv_persistent(const Gemv
     const uint32_t K = w.cols, pw = K / 4;
     const int32_t* x = a.x + (size_t)token * a.x_stride;
 
-    // Tiles in groups of GEMV_WAVES / split; split waves share a tile's blocks.
-    const uint32_t per_group = GEMV_WAVES / split;
+    // Tiles in groups of W / split; split waves share a tile's blocks.
+    const uint32_t per_group = W / split;
     const uint32_t groups = (w.tiles + per_group - 1) / per_group;
     const uint32_t part = wave % split;
     const uint32_t slot = part * 4 + g, nslots = split * 4;
@@ -595,7 +599,7 @@ __global__ __launch_bounds__(GEMV_THREADS, 4) void q8_gemv_persistent(const Gemv
     // Once per workgroup: the norm scale and every digit plane of the row.
     if (tid == 0) s_limbs = 1;
     __syncthreads();
-    const int need = stage_row(a, x, pw, planes, ssq, &s_scale, tid);
+    const int need = stage_row<W * 64>(a, x, pw, planes, ssq, &s_scale, tid);
     const int wave_need = wave_max_int(need);  // one LDS atomic per wave, not per lane
     if (lane == 0) atomicMax(&s_limbs, wave_need);
     __syncthreads();
@@ -682,20 +686,37 @@ void gemv_prepare_once() {
         g_num_cus = prop.multiProcessorCount;
     if (g_num_cus <= 0) g_num_cus = 256;
     const int bytes = MAX_LIMBS * PERSISTENT_MAX_K;
-    hipFuncSetAttribute((const void*)&q8_gemv_persistent<Q8_SCALE_ROW>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    hipFuncSetAttribute((const void*)&q8_gemv_persistent<Q8_SCALE_F16>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-    hipFuncSetAttribute((const void*)&q8_gemv_persistent<Q8_SCALE_I64>, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+    for (const void* f : {(const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 8>, (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 8>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 8>, (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 16>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 16>, (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 16>})
+        hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
 }
 
-// Waves sharing one tile: enough tile groups for every resident workgroup.
-uint32_t choose_split(uint32_t tiles) {
-    if (g_split_override == 1 || g_split_override == 2 || g_split_override == 4 || g_split_override == 8)
+// Waves sharing one tile (of a workgroup's W): enough tile groups for
+// every resident workgroup (wgs of them).
+uint32_t choose_split(uint32_t tiles, uint32_t w, uint64_t wgs) {
+    if (g_split_override == 1 || g_split_override == 2 || g_split_override == 4 || g_split_override == 8 ||
+        (g_split_override == 16 && w == 16))
         return g_split_override;
-    const uint64_t target = (uint64_t)WGS_PER_CU * g_num_cus;
-    for (uint32_t s = 1; s < GEMV_WAVES; s *= 2)
-        if ((uint64_t)tiles * s / GEMV_WAVES >= target) return s;
-    return GEMV_WAVES;
+    for (uint32_t s = 1; s < w; s *= 2)
+        if ((uint64_t)tiles * s / w >= wgs) return s;
+    return w;
+}
+
+template <int W>
+int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) {
+    const uint32_t split = choose_split(a.w.tiles, W, resident);
+    const uint32_t groups = (a.w.tiles + W / split - 1) / (W / split);
+    const uint32_t wgs = min(groups, (uint32_t)resident);
+    const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
+    dim3 grid(wgs, a.tokens);
+    switch (a.w.scale_mode) {
+        case Q8_SCALE_ROW: hipLaunchKernelGGL((q8_gemv_persistent<Q8_SCALE_ROW, W>), grid, dim3(W * 64), shmem, stream, a, split); break;
+        case Q8_SCALE_F16: hipLaunchKernelGGL((q8_gemv_persistent<Q8_SCALE_F16, W>), grid, dim3(W * 64), shmem, stream, a, split); break;
+        default: hipLaunchKernelGGL((q8_gemv_persistent<Q8_SCALE_I64, W>), grid, dim3(W * 64), shmem, stream, a, split); break;
+    }
+    return (int)hipGetLastError();
 }
 
 }  // namespace
@@ -714,17 +735,11 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.tokens > 65535) return IRIS_E_INVALID;
     gemv_prepare_once();
     if (a.w.cols <= PERSISTENT_MAX_K) {
-        const uint32_t split = choose_split(a.w.tiles);
-        const uint32_t groups = (a.w.tiles + GEMV_WAVES / split - 1) / (GEMV_WAVES / split);
-        const uint32_t wgs = min(groups, (uint32_t)(WGS_PER_CU * g_num_cus));
-        const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
-        dim3 grid(wgs, a.tokens);
-        switch (a.w.scale_mode) {
-            case Q8_SCALE_ROW: hipLaunchKernelGGL(q8_gemv_persistent<Q8_SCALE_ROW>, grid, dim3(GEMV_THREADS), shmem, stream, a, split); break;
-            case Q8_SCALE_F16: hipLaunchKernelGGL(q8_gemv_persistent<Q8_SCALE_F16>, grid, dim3(GEMV_THREADS), shmem, stream, a, split); break;
-            default: hipLaunchKernelGGL(q8_gemv_persistent<Q8_SCALE_I64>, grid, dim3(GEMV_THREADS), shmem, stream, a, split); break;
-        }
-        return (int)hipGetLastError();
+        // Long rows (K >= 8192) of a matrix with at most one tile per CU: one
+        // 16-wave workgroup per CU (measured faster there; slower for short rows).
+        if (a.w.tiles <= (uint32_t)g_num_cus && a.w.cols >= 8192)
+            return launch_persistent<16>(a, stream, (uint64_t)g_num_cus);
+        return launch_persistent<8>(a, stream, (uint64_t)WGS_PER_CU * g_num_cus);
     }
     dim3 grid(a.w.tiles, a.tokens);
     switch (a.w.scale_mode) {
