@@ -68,6 +68,18 @@ int q8gpu_upload_q8_0(const uint8_t* blocks, uint32_t rows, uint32_t cols, Q8Gpu
 int q8gpu_product_device(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens,
                          int32_t* d_out, void* stream);
 
+/* Device bytes of work space a `tokens`-token product may use (0 for a
+ * single token). */
+uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* matrix, uint32_t tokens);
+
+/* q8gpu_product_device with caller-provided device work space of at least
+ * q8gpu_workspace_bytes: a multi-token product of a matrix whose blocks share
+ * one scale per row then runs on the int8 matrix cores (same bits). NULL work
+ * space = q8gpu_product_device. Returns IRIS_E_RANGE (-5) when it is too
+ * small. The synchronous q8gpu_product uses its own work space. */
+int q8gpu_product_device_ws(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens,
+                            int32_t* d_out, void* d_workspace, uint64_t workspace_bytes, void* stream);
+
 /* rows, cols and the device layout the upload chose: 0 = one scale per row
  * (every block of each row shares it), 1 = one f16 per block, 2 = one i64 per
  * block; bytes = device memory held. */

@@ -18,7 +18,12 @@ thread_local const char* g_error_text = nullptr;
 std::mutex g_product_lock;
 int32_t* g_scratch_act = nullptr;
 int32_t* g_scratch_out = nullptr;
-size_t g_scratch_act_bytes = 0, g_scratch_out_bytes = 0;
+int32_t* g_scratch_ws = nullptr;  // the MFMA product's digit planes
+size_t g_scratch_act_bytes = 0, g_scratch_out_bytes = 0, g_scratch_ws_bytes = 0;
+
+// Work space of a multi-token product: 5 digit planes of the activations
+// (256-byte aligned), then one digit count per token.
+uint64_t planes_bytes(uint32_t cols, uint32_t tokens) { return (5ull * tokens * cols + 255) & ~255ull; }
 
 hipError_t reserve(int32_t** buf, size_t* cap, size_t bytes) {
     if (bytes <= *cap) return hipSuccess;
@@ -216,6 +221,16 @@ int q8gpu_upload(const int8_t* weights, const int64_t* scales, uint32_t rows, ui
 
 int q8gpu_product_device(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
                          void* stream) {
+    return q8gpu_product_device_ws(m, d_act, tokens, d_out, nullptr, 0, stream);
+}
+
+uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* m, uint32_t tokens) {
+    if (!m || tokens < 2) return 0;
+    return planes_bytes(m->cols, tokens) + 4ull * tokens;
+}
+
+int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
+                            void* d_workspace, uint64_t workspace_bytes, void* stream) {
     if (!m || (tokens && (!d_act || !d_out))) return IRIS_E_INVALID;
     GemvArgs a{};
     a.w = q8_view(m);
@@ -226,6 +241,11 @@ int q8gpu_product_device(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t to
     a.epilogue = EPI_STORE;
     a.out = d_out;
     a.out_stride = m->rows;
+    if (d_workspace && tokens >= 2) {
+        if (workspace_bytes < q8gpu_workspace_bytes(m, tokens)) return IRIS_E_RANGE;
+        a.planes = (int8_t*)d_workspace;
+        a.token_limbs = (int32_t*)((char*)d_workspace + planes_bytes(m->cols, tokens));
+    }
     return iris_gemv_launch(a, (hipStream_t)stream);
 }
 
@@ -235,11 +255,14 @@ int q8gpu_product(const Q8GpuMatrix* m, const int32_t* activations, uint32_t tok
     std::lock_guard<std::mutex> guard(g_product_lock);
     const size_t act_bytes = (size_t)tokens * m->cols * sizeof(int32_t);
     const size_t out_bytes = (size_t)tokens * m->rows * sizeof(int32_t);
+    const size_t ws_bytes = q8gpu_workspace_bytes(m, tokens);
     hipError_t st = reserve(&g_scratch_act, &g_scratch_act_bytes, act_bytes);
     if (st == hipSuccess) st = reserve(&g_scratch_out, &g_scratch_out_bytes, out_bytes);
+    if (st == hipSuccess && ws_bytes) st = reserve(&g_scratch_ws, &g_scratch_ws_bytes, ws_bytes);
     if (st == hipSuccess) st = hipMemcpy(g_scratch_act, activations, act_bytes, hipMemcpyHostToDevice);
     if (st != hipSuccess) return (int)st;
-    int rc = q8gpu_product_device(m, g_scratch_act, tokens, g_scratch_out, nullptr);
+    int rc = q8gpu_product_device_ws(m, g_scratch_act, tokens, g_scratch_out, ws_bytes ? g_scratch_ws : nullptr,
+                                     ws_bytes, nullptr);
     if (rc != 0) return rc;
     st = hipMemcpy(out, g_scratch_out, out_bytes, hipMemcpyDeviceToHost);
     return (int)st;

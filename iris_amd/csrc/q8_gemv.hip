@@ -14,6 +14,7 @@
 // the exact 64-bit block sum.
 #include "detnum_dev.h"
 #include "q8_internal.h"
+#include "q8_epilogue.h"
 
 namespace {
 
@@ -184,45 +185,7 @@ __device__ void finish_tile(const GemvArgs& a, uint32_t tile, uint32_t token, dn
         return;
     }
     if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
-    switch (a.epilogue) {
-        case EPI_RESIDUAL:
-            a.out[(size_t)token * a.out_stride + row] =
-                dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
-            break;
-        case EPI_SOFTCAP:
-            a.out[(size_t)token * a.out_stride + row] = dn::softcap(v, a.softcap);
-            break;
-        case EPI_SWIGLU:
-        case EPI_GEGLU:
-            if ((row & 1) == 0) {
-                const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v) : dn::gelu(v);
-                a.out[(size_t)token * a.out_stride + (row >> 1)] = dn::mul_sat(act, partner);
-            }
-            break;
-        case EPI_ROPE_KV: {
-            const uint32_t pos = (uint32_t)(*a.d_pos) + token;
-            if (row < a.q_rows + a.kv_rows) {
-                if ((row & 1) == 0) {
-                    int32_t x0 = v, x1 = partner;
-                    // mistral.rs:114-126: pair j of each head, position * f_j.
-                    if (pos != 0) dn::rotate_pair_q30(x0, x1, (int64_t)pos * a.inv_freq[(row % a.head_dim) >> 1]);
-                    if (row < a.q_rows) {
-                        a.out[(size_t)token * a.out_stride + row] = x0;
-                        a.out[(size_t)token * a.out_stride + row + 1] = x1;
-                    } else {
-                        int32_t* kc = a.k_cache + (size_t)(row - a.q_rows) * a.k_pos_stride + pos;
-                        kc[0] = x0;
-                        kc[a.k_pos_stride] = x1;
-                    }
-                }
-            } else {
-                a.v_cache[(size_t)pos * a.kv_rows + (row - a.q_rows - a.kv_rows)] = v;
-            }
-            break;
-        }
-        default:
-            a.out[(size_t)token * a.out_stride + row] = v;
-    }
+    store_output(a, row, token, v, partner);
 }
 
 // Stages x[4*i0 .. 4*i1) (after the optional rms_norm: mul_sat(mul_sat(v,
@@ -730,6 +693,7 @@ int iris_select_launch(const GemvArgs& a, hipStream_t stream) {
 
 int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.tokens == 0 || a.w.rows == 0) return 0;
+    if (iris_gemm_applies(a)) return iris_gemm_launch(a, stream);
     if (a.w.cols % 32 || a.x_stride % 4 || ((uintptr_t)a.x & 15)) return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
     if (a.tokens > 65535) return IRIS_E_INVALID;

@@ -105,7 +105,16 @@ struct GemvArgs {
     int32_t* x_next;            // [hidden]
     int32_t* ids_next;          // nullable: the selected id is also stored here
     uint64_t* sel_partial;      // [tiles]: (index << 32) | (uint32)value of each tile's first maximum
+    // Multi-token products of row-scale matrices go through the int8 MFMA
+    // GEMM when this work space is given (null: the GEMV path).
+    int8_t* planes;             // [5 digit planes][tokens][cols]
+    int32_t* token_limbs;       // [tokens]: digits each token's activations need
 };
+
+// The MFMA GEMM for a multi-token product (row-scale matrix, planes set);
+// returns IRIS_E_INVALID when the launch does not qualify.
+int iris_gemm_launch(const GemvArgs& a, hipStream_t stream);
+bool iris_gemm_applies(const GemvArgs& a);
 
 // After an EPI_HEAD_SELECT product with the same arguments: selects the first
 // maximum over the tile partials, writes the token, embeds it as the next

@@ -56,6 +56,15 @@ hipError_t dev_alloc_copy(T** dst, const void* src, size_t bytes) {
 
 }  // namespace
 
+// Multi-row passes hand the products the session's digit-plane work space,
+// which routes row-scale matrices through the MFMA GEMM.
+static inline void with_gemm_space(GemvArgs& g, const IrisSession* s, uint32_t rows) {
+    if (rows > 1) {
+        g.planes = s->planes;
+        g.token_limbs = s->token_limbs;
+    }
+}
+
 // ---------------------------------------------------------------- model
 
 int iris_model_build_layer_if_complete(IrisModel* m, uint32_t l) {
@@ -408,6 +417,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         g.k_cache = s->k_cache[l];
         g.k_pos_stride = s->max_positions;
         g.v_cache = s->v_cache[l];
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 2. attention.
         AttnArgs a{};
@@ -443,6 +453,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         g.out_stride = H;
         g.residual = s->x;
         g.residual_stride = H;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 4. gated = mul(silu(W_gate m), W_up m), m = rms_norm(attended).
         g = GemvArgs{};
@@ -456,6 +467,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         g.epilogue = EPI_SWIGLU;
         g.out = s->gated;
         g.out_stride = d.ffn;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 5. x = W_down gated + attended.
         g = GemvArgs{};
@@ -468,6 +480,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         g.out_stride = H;
         g.residual = s->attended;
         g.residual_stride = H;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         if (layer_rows_out)
             RT_CHECK(hipMemcpyAsync(layer_rows_out + (size_t)l * rows * H, s->x, (size_t)rows * H * 4,
@@ -523,6 +536,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
         g.epilogue = EPI_STORE;
         g.out = s->qkv;
         g.out_stride = qkvw;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 2. per-head norms and RoPE, K/V into the layer's own cache (:607-647)
         GemmaQkvArgs qa{};
@@ -574,6 +588,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
         g.epilogue = EPI_STORE;
         g.out = s->tmp;
         g.out_stride = H;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_attn, d.norm_eps, s->x, H, 0, s->attended, H, H,
                                            rows, st));
@@ -589,6 +604,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
         g.epilogue = EPI_GEGLU;
         g.out = s->gated;
         g.out_stride = L.ffn;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 6. attended = rms_norm(W_down gated, post_ffw) + attended  (finish_mlp :915-929)
         g = GemvArgs{};
@@ -599,6 +615,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
         g.epilogue = EPI_STORE;
         g.out = s->tmp;
         g.out_stride = H;
+        with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ffw, d.norm_eps, s->attended, H, 0, s->attended, H,
                                            H, rows, st));
@@ -740,6 +757,11 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->q, (size_t)max_rows * qw);
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
+    if (max_rows > 1) {
+        size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
+        if (st == hipSuccess) st = hipMalloc((void**)&s->planes, 5 * (size_t)max_rows * widest);
+        alloc(&s->token_limbs, max_rows);
+    }
     if (d.family == IRIS_FAMILY_GEMMA_DENSE) {
         const size_t lp = (size_t)d.layers * d.ple_width;
         alloc(&s->qkv, (size_t)max_rows * m->max_qkv);
@@ -778,6 +800,8 @@ void iris_session_free(IrisSession* s) {
                        s->logits_keep, s->qkv, s->tmp, s->ple_proj, s->ple_rows, s->ple_gated})
         hipFree(p);
     hipFree(s->sel_partial);
+    hipFree(s->planes);
+    hipFree(s->token_limbs);
     hipFree(s->attn_scores);
     hipFree(s->attn_chunk_max);
     hipFree(s->attn_chunk_acc);

@@ -69,6 +69,9 @@ struct IrisSession {
     // gemma-dense only: raw q|k|v rows, a product's rows before their norm,
     // the PLE projections and inputs of every layer, the PLE gate output
     int32_t *qkv = nullptr, *tmp = nullptr, *ple_proj = nullptr, *ple_rows = nullptr, *ple_gated = nullptr;
+    // digit planes of a multi-row pass's activations for the MFMA products
+    int8_t* planes = nullptr;        // [5][max_rows][widest product input]
+    int32_t* token_limbs = nullptr;  // [max_rows]
     int32_t *logits = nullptr, *ids = nullptr, *tokens = nullptr;
     int32_t *d_pos = nullptr, *d_step = nullptr;
     int32_t* logits_keep = nullptr;

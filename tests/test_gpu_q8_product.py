@@ -149,3 +149,25 @@ def test_microbench_gemm_full_size_sampled_rows():
     xs = rand_activations(rng, 64, K, 32)
     got = linear_slab_from_source(xs, m)
     assert np.array_equal(got[:, rows], cpu.linear_q8(xs, raw[rows]))
+
+
+@pytest.mark.parametrize("tokens,rows,cols", [(2, 16, 64), (65, 200, 128), (130, 300, 1536)])
+def test_mfma_product_with_workspace(tokens, rows, cols):
+    # Multi-token products of a row-scale matrix with caller work space run on
+    # the int8 matrix cores; every output against the oracle, with partial
+    # token and row tiles and full-range activations (five digit planes).
+    rng = np.random.default_rng(tokens * 7 + rows)
+    raw = synth.q8_matrix(synth.tensor_seed(9, rows), rows, cols, synth.scale_base_for(cols), True)
+    m = Q8Matrix.from_bytes(raw, rows, cols)
+    assert m.info()["scale_mode"] == "row"
+    L = native.lib()
+    for x in (rand_activations(rng, tokens, cols, 32), rand_activations(rng, tokens, cols, 20)):
+        ws_bytes = L.q8gpu_workspace_bytes(m.handle, tokens)
+        assert ws_bytes >= 5 * tokens * cols
+        dx = native.DeviceBuffer.from_array(x)
+        dout = native.DeviceBuffer(tokens * rows * 4)
+        ws = native.DeviceBuffer(ws_bytes)
+        assert L.q8gpu_product_device_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes - 1, None) == -5
+        native.check(L.q8gpu_product_device_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, None), "product")
+        native.check(L.q8gpu_synchronize(), "sync")
+        assert np.array_equal(dout.to_array(np.int32, (tokens, rows)), cpu.linear_q8(x, raw))
