@@ -193,6 +193,11 @@ int iris_session_layer_pass(IrisSession* session, const int32_t* ids, uint32_t c
 int iris_session_time_decode(IrisSession* session, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,
                              double* ms_per_token, double* prefill_ms, int32_t* out_tokens);
 
+/* Times one pass of every layer over `count` rows at position 0 (the
+ * teacher-forced pass without downloading rows or hashing) with HIP events
+ * on the session's stream. */
+int iris_session_time_pass(IrisSession* session, const int32_t* ids, uint32_t count, double* ms);
+
 /* SHA-256 (FIPS 180-4) of `len` bytes into out[32]; the hash
  * iris_session_layer_pass uses. Host code only. */
 int iris_sha256_bytes(const uint8_t* data, uint64_t len, uint8_t* out);

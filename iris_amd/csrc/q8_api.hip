@@ -23,7 +23,7 @@ size_t g_scratch_act_bytes = 0, g_scratch_out_bytes = 0, g_scratch_ws_bytes = 0;
 
 // Work space of a multi-token product: 5 digit planes of the activations
 // (256-byte aligned), then one digit count per token.
-uint64_t planes_bytes(uint32_t cols, uint32_t tokens) { return (5ull * tokens * cols + 255) & ~255ull; }
+uint64_t planes_bytes(uint32_t cols, uint32_t tokens) { return gemm_planes_bytes(cols, tokens); }
 
 hipError_t reserve(int32_t** buf, size_t* cap, size_t bytes) {
     if (bytes <= *cap) return hipSuccess;

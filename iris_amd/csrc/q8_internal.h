@@ -107,9 +107,15 @@ struct GemvArgs {
     uint64_t* sel_partial;      // [tiles]: (index << 32) | (uint32)value of each tile's first maximum
     // Multi-token products of row-scale matrices go through the int8 MFMA
     // GEMM when this work space is given (null: the GEMV path).
-    int8_t* planes;             // [5 digit planes][tokens][cols]
+    int8_t* planes;             // gemm_planes_bytes(cols, tokens): 5 digit planes, MFMA-operand tiled
     int32_t* token_limbs;       // [tokens]: digits each token's activations need
 };
+
+// Bytes of the MFMA product's digit planes: 5 planes of the tokens rounded
+// up to whole 16-token tiles, times cols, 256-byte aligned.
+inline uint64_t gemm_planes_bytes(uint32_t cols, uint32_t tokens) {
+    return (5ull * ((tokens + 15ull) & ~15ull) * cols + 255) & ~255ull;
+}
 
 // The MFMA GEMM for a multi-token product (row-scale matrix, planes set);
 // returns IRIS_E_INVALID when the launch does not qualify.

@@ -759,7 +759,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
     if (max_rows > 1) {
         size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
-        if (st == hipSuccess) st = hipMalloc((void**)&s->planes, 5 * (size_t)max_rows * widest);
+        if (st == hipSuccess) st = hipMalloc((void**)&s->planes, gemm_planes_bytes((uint32_t)widest, max_rows));
         alloc(&s->token_limbs, max_rows);
     }
     if (d.family == IRIS_FAMILY_GEMMA_DENSE) {
@@ -883,6 +883,25 @@ int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, 
             iris_sha256((const uint8_t*)(dst + (size_t)l * count * d.hidden), (size_t)count * d.hidden * 4,
                         out_hashes + 32 * l);
     return 0;
+}
+
+int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, double* ms) {
+    if (!s || !ids || !ms || count == 0) return IRIS_E_INVALID;
+    if (count > s->max_rows || count > s->model->d.max_positions) return IRIS_E_RANGE;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    RT_CHECK(hipEventCreate(&e0));
+    RT_CHECK(hipEventCreate(&e1));
+    int rc = session_reset_and_embed(s, ids, count);
+    if (rc == 0) rc = (int)hipEventRecord(e0, s->stream);
+    if (rc == 0) rc = session_pass(s, count, nullptr);
+    if (rc == 0) rc = (int)hipEventRecord(e1, s->stream);
+    float t = 0.f;
+    if (rc == 0) rc = (int)hipEventSynchronize(e1);
+    if (rc == 0) rc = (int)hipEventElapsedTime(&t, e0, e1);
+    hipEventDestroy(e0);
+    hipEventDestroy(e1);
+    if (rc == 0) *ms = t;
+    return rc;
 }
 
 int iris_session_time_decode(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,

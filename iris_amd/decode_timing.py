@@ -105,6 +105,31 @@ class DecodeBench:
         return MISTRAL_7B_WEIGHT_BYTES + 2 * 4 * kvw * s.num_hidden_layers * mean_ctx
 
 
+def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None) -> dict:
+    """One pass of every layer over `rows` uniform-random token ids at
+    Mistral-7B shape: the device time of the pass alone (HIP events), and
+    the wall time of the full per-layer checkpoint call (pass, rows copied
+    to the host, one SHA-256 per layer)."""
+    import time
+    log = log or (lambda msg: None)
+    model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
+    dm = DeviceModel(model)
+    vocab = model.vocab
+    del model.tensors
+    log("model on device")
+    session = Session(dm, rows, rows)
+    ids = synth.token_ids(PROMPT_SEED, rows, vocab)
+    device_ms = [session.time_pass(ids) for _ in range(repeats)]
+    log(f"device pass ms {device_ms}")
+    t = time.perf_counter()
+    _, hashes = session.layer_pass(ids, keep_rows=False)
+    wall_ms = (time.perf_counter() - t) * 1e3
+    session.free()
+    dm.free()
+    return {"rows": rows, "device_ms": min(device_ms), "checkpoint_wall_ms": wall_ms,
+            "layers": len(hashes), "last_hash": hashes[-1]}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
     ap.add_argument("--steps", type=int, default=PROMPT - 1)
@@ -112,8 +137,14 @@ def main(argv=None):
     ap.add_argument("--gemv-only", action="store_true", help="time only the Q8_0 GEMV")
     ap.add_argument("--calibrate", action="store_true",
                     help="first run a 256 MiB device-to-device copy (byte-counter calibration)")
+    ap.add_argument("--pass-rows", type=int, default=0,
+                    help="time only the teacher-forced pass over this many rows")
     args = ap.parse_args(argv)
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    if args.pass_rows:
+        r = time_teacher_forced(args.pass_rows, log=lambda m: print(m, file=sys.stderr, flush=True))
+        print(json.dumps(r), flush=True)
+        return
     if args.calibrate:
         copy_calibration()
     if args.gemv_only:

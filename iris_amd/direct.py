@@ -51,6 +51,7 @@ def _declare():
         "iris_session_generate": (C.c_int, [vp, vp, u32, u32, vp, u32, vp, C.POINTER(u32), vp, i32]),
         "iris_session_layer_pass": (C.c_int, [vp, vp, u32, vp, vp]),
         "iris_session_time_decode": (C.c_int, [vp, vp, u32, u32, C.POINTER(C.c_double), C.POINTER(C.c_double), vp]),
+        "iris_session_time_pass": (C.c_int, [vp, vp, u32, C.POINTER(C.c_double)]),
         "iris_sha256_bytes": (C.c_int, [vp, u64, vp]),
     }
     for name, (res, args) in sig.items():
@@ -195,6 +196,14 @@ class Session:
                                                            C.byref(ms), C.byref(pre), toks.ctypes.data),
                      "time decode")
         return ms.value, pre.value, toks.tolist()
+
+    def time_pass(self, ids) -> float:
+        """Milliseconds of one pass of every layer over ``ids`` (HIP events)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        ms = C.c_double()
+        native.check(native.lib().iris_session_time_pass(self._h, ids.ctypes.data, ids.size, C.byref(ms)),
+                     "time pass")
+        return ms.value
 
     def free(self):
         if getattr(self, "_h", None):

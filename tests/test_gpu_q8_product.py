@@ -4,7 +4,8 @@ Cases follow the reference's own device tests
 (crates/inference/kernels/src/gpu.rs:374-495): shapes on and across tiles,
 three magnitude regimes including i32::MIN/MAX activations, exact ties, a
 matrix uploaded through both entry points, and non-finite scales refused.
-Plus the microbenchmark's full sizes.
+Plus the microbenchmark's full sizes (the M=1 GEMV at K=4096, N=14336 and
+the M=512 GEMM at K=N=4096).
 """
 import numpy as np
 import pytest
@@ -171,3 +172,38 @@ def test_mfma_product_with_workspace(tokens, rows, cols):
         native.check(L.q8gpu_product_device_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, None), "product")
         native.check(L.q8gpu_synchronize(), "sync")
         assert np.array_equal(dout.to_array(np.int32, (tokens, rows)), cpu.linear_q8(x, raw))
+
+
+def grouped_activations(rng, tokens, cols):
+    """Token group g (128 tokens each) needs exactly 1, 2, 3, 4, 5 digits for
+    g = 0..4: magnitudes of 8, 15, 23 and 31 bits, then the full range with
+    i32::MAX / i32::MIN at 1/61 of positions."""
+    x = np.empty((tokens, cols), np.int32)
+    for g0 in range(0, tokens, 128):
+        g = (g0 // 128) % 5
+        n = min(128, tokens - g0)
+        if g < 4:
+            b = (8, 15, 23, 31)[g]
+            x[g0:g0 + n] = rng.integers(-(1 << (b - 1)), 1 << (b - 1), (n, cols))
+        else:
+            x[g0:g0 + n] = rand_activations(rng, n, cols, 32)
+    return x
+
+
+@pytest.mark.parametrize("tokens,rows,cols", [(603, 1024, 192), (603, 136, 4160), (300, 272, 64)])
+def test_mfma_product_digit_paths(tokens, rows, cols):
+    # Every digit count's code path (one to three planes side by side, four
+    # and five in two token halves), one-step, short and long k loops, and
+    # launches whose block count does and does not split evenly over the XCDs.
+    rng = np.random.default_rng(tokens + rows + cols)
+    raw = synth.q8_matrix(synth.tensor_seed(11, rows), rows, cols, synth.scale_base_for(cols), True)
+    m = Q8Matrix.from_bytes(raw, rows, cols)
+    L = native.lib()
+    x = grouped_activations(rng, tokens, cols)
+    ws_bytes = L.q8gpu_workspace_bytes(m.handle, tokens)
+    dx = native.DeviceBuffer.from_array(x)
+    dout = native.DeviceBuffer(tokens * rows * 4)
+    ws = native.DeviceBuffer(ws_bytes)
+    native.check(L.q8gpu_product_device_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, None), "product")
+    native.check(L.q8gpu_synchronize(), "sync")
+    assert np.array_equal(dout.to_array(np.int32, (tokens, rows)), cpu.linear_q8(x, raw))
