@@ -1,6 +1,6 @@
 """Benchmark: exact Q8_0 greedy decode at Mistral-7B shape on one MI355X.
 
-The workload is the north-star decode configuration: 32 mistral-dense layers
+The workload is the Mistral-7B-shape decode: 32 mistral-dense layers
 (hidden 4096, 32 query / 8 KV heads of 128, SwiGLU 14336, vocab 32000,
 RoPE base 1e6), random-init Q8_0 weights from a seed, a 512-token prompt and
 greedy decoding at batch 1. One step is one decode pass (every layer and the

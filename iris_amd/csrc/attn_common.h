@@ -1,0 +1,167 @@
+// Shared pieces of the attention kernels: first-maximum and saturating
+// reductions, and the scalar attention of one (head, query row) that the
+// multi-row paths fall back on.
+#pragma once
+
+#include "detnum_dev.h"
+#include "layer_kernels.h"
+
+namespace {
+
+constexpr int ATTN_MAX_THREADS = 1024;
+constexpr int ATTN_MAX_WAVES = ATTN_MAX_THREADS / 64;
+
+struct ArgMax {
+    int32_t v;
+    uint32_t i;
+};
+
+// First maximum: larger value wins, equal values keep the smaller index
+// (crates/det-num/src/ops.rs:466-481; crates/inference/direct/src/generation.rs:25-33).
+__device__ __forceinline__ ArgMax argmax_combine(ArgMax a, ArgMax b) {
+    if (b.v > a.v || (b.v == a.v && b.i < a.i)) return b;
+    return a;
+}
+
+__device__ __forceinline__ ArgMax wave_argmax(ArgMax a) {
+    for (int off = 32; off >= 1; off >>= 1) {
+        ArgMax o{__shfl_xor(a.v, off), (uint32_t)__shfl_xor((int)a.i, off)};
+        a = argmax_combine(a, o);
+    }
+    return a;
+}
+
+__device__ __forceinline__ int64_t wave_sum_sat64(int64_t v) {
+    for (int off = 32; off >= 1; off >>= 1) v = dn::acc_add_sat(v, __shfl_xor(v, off));
+    return v;
+}
+
+__device__ __forceinline__ int32_t wave_sum_sat32(int32_t v) {
+    for (int off = 32; off >= 1; off >>= 1) v = dn::add_sat(v, __shfl_xor(v, off));
+    return v;
+}
+
+// The LDS one attend_row call uses.
+struct AttnRowSmem {
+    int32_t w[ATTN_MAX_KEYS];
+    int64_t e[ATTN_MAX_KEYS];
+    int32_t q[ATTN_MAX_HEAD_DIM];
+    int64_t part[ATTN_MAX_THREADS];
+    ArgMax am[ATTN_MAX_WAVES];
+    int64_t sum[ATTN_MAX_WAVES];
+    int32_t wsum[ATTN_MAX_WAVES];
+};
+
+// One (query head, query row) by the whole workgroup of blockDim.x threads (a
+// multiple of 256, at most 1024, at least head_dim). Scores over the visible keys: each round takes
+// 64 * waves/4 keys, one key per lane and a quarter of the head's dimensions
+// per wave (independent coalesced loads from the transposed K cache), the four
+// quarters summed through LDS. Then the det-num softmax (ops.rs:233-261) and
+// the weighted values (ops.rs:339-355; mistral/layer.rs:304-315;
+// prefill_range.rs:816-844), one head dimension per thread.
+__device__ inline void attend_row(const AttnArgs& a, uint32_t head, uint32_t token, AttnRowSmem& sm) {
+    constexpr uint32_t QS = 4;  // dimension quarters per key
+    int32_t* s_w = sm.w;
+    int64_t* s_e = sm.e;
+    int32_t* s_q = sm.q;
+    int64_t* s_part = sm.part;
+    ArgMax* s_am = sm.am;
+    int64_t* s_sum = sm.sum;
+    int32_t* s_wsum = sm.wsum;
+
+    const uint32_t nthreads = blockDim.x, nwaves = nthreads / 64;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t hd = a.head_dim, dq = hd / QS;
+    const uint32_t kvh = head / (a.heads / a.kv_heads);
+    const uint32_t pos = (uint32_t)(*a.d_pos) + token;
+    const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
+    const uint32_t n = pos - start + 1;
+    const int32_t* q = a.q + (size_t)token * a.q_stride + (size_t)head * hd;
+    for (uint32_t d = tid; d < hd; d += nthreads) s_q[d] = q[d];
+    __syncthreads();
+
+    // Scores, and the first maximum of the keys this thread finishes.
+    const uint32_t per_round = 64 * (nwaves / QS);
+    const uint32_t kg = wave / QS, qd = wave % QS;
+    const int32_t* kt = a.k_cache + ((size_t)kvh * hd + (size_t)qd * dq) * a.k_pos_stride + start;
+    ArgMax best{INT32_MIN, 0xffffffffu};
+    for (uint32_t base = 0; base < n; base += per_round) {
+        const uint32_t key = base + kg * 64 + lane;
+        uint64_t acc = 0;  // wrapping i64 (mac_bits, ops.rs:17-19)
+        if (key < n) {
+            const int32_t* kk = kt + key;
+#pragma unroll 16
+            for (uint32_t i = 0; i < dq; i++)
+                acc += (uint64_t)((int64_t)s_q[qd * dq + i] * kk[(size_t)i * a.k_pos_stride]);
+        }
+        s_part[qd * per_round + kg * 64 + lane] = (int64_t)acc;
+        __syncthreads();
+        if (tid < per_round && base + tid < n) {
+            uint64_t sum = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < QS; i++) sum += (uint64_t)s_part[i * per_round + tid];
+            const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)sum, a.scale_q32)
+                                        : dn::requantize((int64_t)sum);
+            s_w[base + tid] = sc;
+            best = argmax_combine(best, ArgMax{sc, base + tid});
+        }
+        __syncthreads();
+    }
+    best = wave_argmax(best);
+    if (lane == 0) s_am[wave] = best;
+    __syncthreads();
+    ArgMax m = s_am[0];
+    for (uint32_t i = 1; i < nwaves; i++) m = argmax_combine(m, s_am[i]);
+
+    // exp terms and their saturating sum (non-negative terms: order-free).
+    int64_t part = 0;
+    for (uint32_t j = tid; j < n; j += nthreads) {
+        const int64_t delta = (int64_t)dn::sub_sat(s_w[j], m.v) * 65536;
+        const int64_t e = dn::softmax_exp_term(delta);
+        s_e[j] = e;
+        part = dn::acc_add_sat(part, e);
+    }
+    part = wave_sum_sat64(part);
+    if (lane == 0) s_sum[wave] = part;
+    __syncthreads();
+    int64_t total = 0;
+    for (uint32_t i = 0; i < nwaves; i++) total = dn::acc_add_sat(total, s_sum[i]);
+
+    // weights requantize(div_acc(e, sum)) and their saturating sum.
+    int32_t wpart = 0;
+    for (uint32_t j = tid; j < n; j += nthreads) {
+        const int32_t w = dn::requantize(dn::div_acc_softmax((uint64_t)s_e[j], (uint64_t)total));
+        s_w[j] = w;
+        wpart = dn::add_sat(wpart, w);
+    }
+    wpart = wave_sum_sat32(wpart);
+    if (lane == 0) s_wsum[wave] = wpart;
+    __syncthreads();
+    if (tid == 0) {
+        int32_t ws = 0;
+        for (uint32_t i = 0; i < nwaves; i++) ws = dn::add_sat(ws, s_wsum[i]);
+        s_w[m.i] = dn::add_sat(s_w[m.i], dn::sub_sat(dn::ONE_ACT, ws));
+    }
+    __syncthreads();
+
+    // ctx[d] = requantize(sum_j w_j v_j[d]), wrapping i64; the keys are split
+    // over nthreads / head_dim groups of threads.
+    const uint32_t groups = nthreads / hd;
+    const uint32_t grp = tid / hd, d = tid % hd;
+    uint64_t acc = 0;
+    if (grp < groups) {
+        const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * hd + d;
+#pragma unroll 8
+        for (uint32_t j = grp; j < n; j += groups) acc += (uint64_t)((int64_t)s_w[j] * vb[(size_t)j * a.kv_stride]);
+    }
+    s_part[tid] = (int64_t)acc;
+    __syncthreads();
+    if (tid < hd) {
+        uint64_t t = 0;
+        for (uint32_t i = 0; i < groups; i++) t += (uint64_t)s_part[i * hd + tid];
+        a.ctx[(size_t)token * a.ctx_stride + (size_t)head * hd + tid] = dn::requantize((int64_t)t);
+    }
+    __syncthreads();
+}
+
+}  // namespace

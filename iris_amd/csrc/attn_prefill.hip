@@ -1,0 +1,439 @@
+// Exact multi-row attention on gfx950's int8 matrix cores.
+//
+// The reference attends one query row at a time (mistral/layer.rs:274-318,
+// prefill_range.rs:755-845): wrapping-i64 scores q.k, the det-num softmax
+// (ops.rs:233-261) and wrapping-i64 weighted values, each requantized. Both
+// sums are exact integers modulo 2^64, so they may be formed in any order.
+// Here queries, keys and values are split into signed byte digits
+// (v = sum_l 256^l d_l, d_l in [-128, 127]) and every pair of digit planes
+// is an int8 MFMA with exact int32 accumulation; the planes are recombined
+// modulo 2^64 (planes whose digit sums share l1 + l2 share an accumulator:
+// |sum| <= 4 * 128 * 2^14 < 2^31 for scores, 2 * 4096 * 2^14 for values).
+//
+// The softmax needs each row's first maximum before any exp term and the
+// full sum before any weight, so each workgroup walks its keys three times,
+// recomputing the scores (cheap on the matrix cores) instead of storing them:
+// (1) the first maximum, (2) the sum of exp terms, (3) the weights and the
+// weighted values. The weights never leave registers: the score tile's lane
+// layout is, up to a fixed permutation of the keys inside each 64-key step,
+// the A operand of the value product, and the value planes are written in
+// that permuted key order. A weight w < 2^16 is two digits unless
+// w >= 32640; those (at most two per row: the weights sum to 2^16 plus
+// rounding) are carried as w - 65536 plus 65536 * v added at the end, with
+// the residual of the first maximum (ops.rs:258-260).
+//
+// Workgroup: one 16-row query tile of four query heads that share a KV head,
+// one wave per head. A tile whose queries or keys need five digits (|v|
+// near i32::MAX), or whose values need four (|v| >= 2^23), takes the scalar
+// one-row routine instead.
+#include "attn_common.h"
+#include "detnum_dev.h"
+#include "layer_kernels.h"
+
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int AP_PLANES = 4;             // digit planes kept per value
+constexpr int AP_V_PLANES = 3;           // value digits the matrix-core path takes (more: scalar path)
+constexpr int32_t BIG_WEIGHT = 32640;    // first weight that needs a third digit
+constexpr uint32_t FRAG = 1024;          // one 16 x 64 MFMA operand
+
+__device__ __forceinline__ uint64_t digits5(int32_t v) {
+    return (uint64_t)((int64_t)v + 0x8080808080LL) ^ 0x8080808080ULL;
+}
+
+__device__ __forceinline__ int limbs_needed(uint64_t d) {
+    return (d >> 32) ? 5 : (d >> 24) ? 4 : (d >> 16) ? 3 : (d >> 8) ? 2 : 1;
+}
+
+// Byte l of the digits of four values, as one dword.
+__device__ __forceinline__ uint32_t digit_dword(const uint64_t (&d)[4], int l) {
+    const int sh = 8 * l;
+    return (uint32_t)((d[0] >> sh) & 0xff) | ((uint32_t)((d[1] >> sh) & 0xff) << 8) |
+           ((uint32_t)((d[2] >> sh) & 0xff) << 16) | ((uint32_t)((d[3] >> sh) & 0xff) << 24);
+}
+
+__device__ __forceinline__ int wave_max_int(int v) {
+    for (int off = 32; off >= 1; off >>= 1) v = max(v, __shfl_xor(v, off));
+    return v;
+}
+
+// Query planes: one wave per (16-row tile, head). Lane l takes row l % 16
+// and dims 16 * (l / 16) .. + 16 of each 64-dim step.
+template <uint32_t HD>
+__global__ __launch_bounds__(64) void attn_q_planes_kernel(const AttnArgs a, uint32_t tokens) {
+    constexpr uint32_t DS = HD / 64;
+    const AttnPlanes& p = a.planes;
+    const uint32_t qt = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const uint32_t t = qt * 16 + (lane & 15), dq = (lane >> 4) * 16;
+    const bool valid = t < tokens;
+    const int32_t* q = a.q + (size_t)(valid ? t : 0) * a.q_stride + (size_t)h * HD;
+    const size_t lstride = (size_t)a.heads * p.qt_cap * DS * FRAG;
+    int need = 1;
+#pragma unroll
+    for (uint32_t ds = 0; ds < DS; ds++) {
+        uint32_t out[AP_PLANES][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            int4 v = make_int4(0, 0, 0, 0);
+            if (valid) v = *(const int4*)(q + ds * 64 + dq + 4 * c);
+            const uint64_t d[4] = {digits5(v.x), digits5(v.y), digits5(v.z), digits5(v.w)};
+            need = max(need, max(max(limbs_needed(d[0]), limbs_needed(d[1])), max(limbs_needed(d[2]), limbs_needed(d[3]))));
+#pragma unroll
+            for (int l = 0; l < AP_PLANES; l++) out[l][c] = digit_dword(d, l);
+        }
+        int8_t* dst = p.q + (((size_t)h * p.qt_cap + qt) * DS + ds) * FRAG + lane * 16;
+#pragma unroll
+        for (int l = 0; l < AP_PLANES; l++)
+            *(uint4*)(dst + l * lstride) = make_uint4(out[l][0], out[l][1], out[l][2], out[l][3]);
+    }
+    need = wave_max_int(need);
+    if (lane == 0) p.q_limbs[h * p.qt_cap + qt] = (uint8_t)need;
+}
+
+// Key and value planes of one 64-key step of one KV head (keys past the
+// last position are zero). Wave w writes key tile w: lane l takes key
+// l % 16 and dims 16 * (l / 16) .. of each 64-dim step. Value d-tiles
+// w, w + 4, ...: lane l takes dim l % 16 and, as byte 4t + i, the key
+// 16t + 4(l / 16) + i of the step.
+template <uint32_t HD>
+__global__ __launch_bounds__(256) void attn_kv_planes_kernel(const AttnArgs a, uint32_t tokens) {
+    constexpr uint32_t DS = HD / 64, DT = HD / 16;
+    __shared__ int s_need[2];
+    const AttnPlanes& p = a.planes;
+    const uint32_t ks = blockIdx.x, g = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t nkeys = (uint32_t)(*a.d_pos) + tokens;
+    if (ks * 64 >= nkeys) return;
+    if (tid < 2) s_need[tid] = 1;
+    __syncthreads();
+
+    const uint32_t key = ks * 64 + wave * 16 + (lane & 15), dq = (lane >> 4) * 16;
+    const bool kvalid = key < nkeys;
+    const size_t kl = (size_t)a.kv_heads * p.ks_cap * 4 * DS * FRAG;
+    int kneed = 1;
+#pragma unroll
+    for (uint32_t ds = 0; ds < DS; ds++) {
+        uint32_t out[AP_PLANES][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            int32_t v[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t dim = ds * 64 + dq + 4 * c + j;
+                v[j] = kvalid ? a.k_cache[((size_t)g * HD + dim) * a.k_pos_stride + key] : 0;
+            }
+            const uint64_t d[4] = {digits5(v[0]), digits5(v[1]), digits5(v[2]), digits5(v[3])};
+            kneed = max(kneed, max(max(limbs_needed(d[0]), limbs_needed(d[1])), max(limbs_needed(d[2]), limbs_needed(d[3]))));
+#pragma unroll
+            for (int l = 0; l < AP_PLANES; l++) out[l][c] = digit_dword(d, l);
+        }
+        int8_t* dst = p.k + (((size_t)g * p.ks_cap * 4 + ks * 4 + wave) * DS + ds) * FRAG + lane * 16;
+#pragma unroll
+        for (int l = 0; l < AP_PLANES; l++)
+            *(uint4*)(dst + l * kl) = make_uint4(out[l][0], out[l][1], out[l][2], out[l][3]);
+    }
+
+    const size_t vl = (size_t)a.kv_heads * p.ks_cap * DT * FRAG;
+    const uint32_t gk = lane >> 4;
+    int vneed = 1;
+    for (uint32_t dt = wave; dt < DT; dt += 4) {
+        const uint32_t dim = dt * 16 + (lane & 15);
+        uint32_t out[AP_PLANES][4];
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            int32_t v[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t k = ks * 64 + 16 * t + 4 * gk + i;
+                v[i] = k < nkeys ? a.v_cache[(size_t)k * a.kv_stride + (size_t)g * HD + dim] : 0;
+            }
+            const uint64_t d[4] = {digits5(v[0]), digits5(v[1]), digits5(v[2]), digits5(v[3])};
+            vneed = max(vneed, max(max(limbs_needed(d[0]), limbs_needed(d[1])), max(limbs_needed(d[2]), limbs_needed(d[3]))));
+#pragma unroll
+            for (int l = 0; l < AP_PLANES; l++) out[l][t] = digit_dword(d, l);
+        }
+        int8_t* dst = p.v + (((size_t)g * p.ks_cap + ks) * DT + dt) * FRAG + lane * 16;
+#pragma unroll
+        for (int l = 0; l < AP_PLANES; l++)
+            *(uint4*)(dst + l * vl) = make_uint4(out[l][0], out[l][1], out[l][2], out[l][3]);
+    }
+    kneed = wave_max_int(kneed);
+    vneed = wave_max_int(vneed);
+    if (lane == 0) {
+        atomicMax(&s_need[0], kneed);
+        atomicMax(&s_need[1], vneed);
+    }
+    __syncthreads();
+    if (tid < 2) p.kv_limbs[((size_t)g * p.ks_cap + ks) * 2 + tid] = (uint8_t)s_need[tid];
+}
+
+struct PrefillSmem {
+    int32_t info[4][16][2];   // per wave and query row: first-maximum key, residual
+    int32_t big[4][16][8];    // per wave and query row: large-weight keys (two per lane group, -1 none)
+};
+
+// The scores of one 16-key tile against the wave's 16 query rows: lane l
+// holds query l % 16 and keys 4 * (l / 16) + i of the tile.
+template <uint32_t HD>
+__device__ __forceinline__ void tile_scores(const AttnArgs& a, const int8_t* kb, size_t kl, int Lk, int Lq,
+                                            const v4i (&qf)[AP_PLANES][HD / 64], int32_t (&sc)[4]) {
+    constexpr uint32_t DS = HD / 64;
+    v4i acc[2 * AP_PLANES - 1];
+#pragma unroll
+    for (int s = 0; s < 2 * AP_PLANES - 1; s++) acc[s] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int l = 0; l < AP_PLANES; l++) {
+        if (l < Lk) {
+#pragma unroll
+            for (uint32_t ds = 0; ds < DS; ds++) {
+                const v4i kf = *(const v4i*)(kb + l * kl + ds * FRAG);
+#pragma unroll
+                for (int b = 0; b < AP_PLANES; b++)
+                    if (b < Lq) acc[l + b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[b][ds], acc[l + b], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        uint64_t s = 0;  // the wrapping i64 dot product
+#pragma unroll
+        for (int j = 0; j < 2 * AP_PLANES - 1; j++) s += (uint64_t)(int64_t)acc[j][i] << (8 * j);
+        sc[i] = a.scaled ? dn::scaled_score_from_sum((int64_t)s, a.scale_q32) : dn::requantize((int64_t)s);
+    }
+}
+
+template <uint32_t HD>
+__global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
+    constexpr uint32_t DS = HD / 64, DT = HD / 16;
+    __shared__ union {
+        AttnRowSmem row;
+        PrefillSmem pre;
+    } sm;
+    __shared__ int s_scalar;
+    const AttnPlanes& p = a.planes;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t group = a.heads / a.kv_heads, hblocks = group / 4, per_qt = a.kv_heads * hblocks;
+    const uint32_t QT = (tokens + 15) / 16;
+    const uint32_t qt = QT - 1 - blockIdx.x / per_qt;  // the longest rows first
+    const uint32_t rest = blockIdx.x % per_qt, g = rest / hblocks, h0 = g * group + (rest % hblocks) * 4;
+    const uint32_t head = h0 + wave;
+    const uint32_t pos0 = (uint32_t)(*a.d_pos);
+    const uint32_t rows = min(16u, tokens - qt * 16);
+    const uint32_t first_pos = pos0 + qt * 16, last_pos = first_pos + rows - 1;
+    const uint32_t first_key = (a.window == 0 || first_pos + 1 <= a.window) ? 0 : first_pos + 1 - a.window;
+    const uint32_t ks0 = first_key / 64, ks1 = last_pos / 64 + 1;
+    const uint8_t* kvl = p.kv_limbs + (size_t)g * p.ks_cap * 2;
+
+    if (tid == 0) s_scalar = 0;
+    __syncthreads();
+    if (tid < 4 && p.q_limbs[(h0 + tid) * p.qt_cap + qt] > AP_PLANES) s_scalar = 1;
+    for (uint32_t ks = ks0 + tid; ks < ks1; ks += 256)
+        if (kvl[2 * ks] > AP_PLANES || kvl[2 * ks + 1] > AP_V_PLANES) s_scalar = 1;
+    __syncthreads();
+    if (s_scalar) {
+        for (uint32_t i = 0; i < 4 * rows; i++) attend_row(a, h0 + i / rows, qt * 16 + i % rows, sm.row);
+        return;
+    }
+
+    // This lane's query row for the scores, and its visible keys.
+    const uint32_t qrow = qt * 16 + (lane & 15), grp = lane >> 4;
+    const bool qvalid = qrow < tokens;
+    const uint32_t qpos = pos0 + qrow;
+    const uint32_t qstart = (a.window == 0 || qpos + 1 <= a.window) ? 0 : qpos + 1 - a.window;
+    const int Lq = p.q_limbs[head * p.qt_cap + qt];
+    v4i qf[AP_PLANES][DS];
+    {
+        const int8_t* qb = p.q + ((size_t)head * p.qt_cap + qt) * DS * FRAG + lane * 16;
+        const size_t ql = (size_t)a.heads * p.qt_cap * DS * FRAG;
+#pragma unroll
+        for (int b = 0; b < AP_PLANES; b++)
+#pragma unroll
+            for (uint32_t ds = 0; ds < DS; ds++) qf[b][ds] = *(const v4i*)(qb + b * ql + ds * FRAG);
+    }
+    const size_t kl = (size_t)a.kv_heads * p.ks_cap * 4 * DS * FRAG;
+    const int8_t* kbase = p.k + (size_t)g * p.ks_cap * 4 * DS * FRAG + lane * 16;
+    auto visible = [&](uint32_t key) { return qvalid && key >= qstart && key <= qpos; };
+
+    // (1) the first maximum: keys run in increasing order in each lane.
+    int32_t best = INT32_MIN;
+    uint32_t best_key = 0xffffffffu;
+    for (uint32_t ks = ks0; ks < ks1; ks++) {
+        const int Lk = kvl[2 * ks];
+#pragma unroll
+        for (uint32_t t = 0; t < 4; t++) {
+            int32_t sc[4];
+            tile_scores<HD>(a, kbase + (size_t)(ks * 4 + t) * DS * FRAG, kl, Lk, Lq, qf, sc);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t key = ks * 64 + 16 * t + 4 * grp + i;
+                if (visible(key) && sc[i] > best) {
+                    best = sc[i];
+                    best_key = key;
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 16; off <= 32; off <<= 1) {
+        const int32_t ov = __shfl_xor(best, off);
+        const uint32_t ok = (uint32_t)__shfl_xor((int)best_key, off);
+        if (ov > best || (ov == best && ok < best_key)) {
+            best = ov;
+            best_key = ok;
+        }
+    }
+
+    // (2) the sum of exp terms (non-negative, so no order and no saturation).
+    uint64_t sum = 0;
+    for (uint32_t ks = ks0; ks < ks1; ks++) {
+        const int Lk = kvl[2 * ks];
+#pragma unroll
+        for (uint32_t t = 0; t < 4; t++) {
+            int32_t sc[4];
+            tile_scores<HD>(a, kbase + (size_t)(ks * 4 + t) * DS * FRAG, kl, Lk, Lq, qf, sc);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t key = ks * 64 + 16 * t + 4 * grp + i;
+                if (visible(key)) sum += dn::softmax_exp_diff((uint32_t)((int64_t)best - sc[i] > (1 << 20) ? (1 << 20) : (int64_t)best - sc[i]));
+            }
+        }
+    }
+    sum += __shfl_xor(sum, 16);
+    sum += __shfl_xor(sum, 32);
+    const double inv_sum = qvalid ? 1.0 / (double)sum : 0.0;
+
+    // (3) weights, their sum, and the weighted values.
+    v4i pacc[DT][AP_V_PLANES + 1];
+#pragma unroll
+    for (uint32_t dt = 0; dt < DT; dt++)
+#pragma unroll
+        for (int s = 0; s < AP_V_PLANES + 1; s++) pacc[dt][s] = v4i{0, 0, 0, 0};
+    const size_t vl = (size_t)a.kv_heads * p.ks_cap * DT * FRAG;
+    const int8_t* vbase = p.v + (size_t)g * p.ks_cap * DT * FRAG + lane * 16;
+    int32_t wsum = 0;
+    int32_t big[2] = {-1, -1};
+    for (uint32_t ks = ks0; ks < ks1; ks++) {
+        const int Lk = kvl[2 * ks], Lv = kvl[2 * ks + 1];
+        uint32_t wd[2][4];  // the two weight digits of this lane's 16 keys, byte 4t + i
+#pragma unroll
+        for (uint32_t t = 0; t < 4; t++) {
+            int32_t sc[4];
+            tile_scores<HD>(a, kbase + (size_t)(ks * 4 + t) * DS * FRAG, kl, Lk, Lq, qf, sc);
+            uint32_t b0 = 0, b1 = 0;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const uint32_t key = ks * 64 + 16 * t + 4 * grp + i;
+                int32_t w = 0;
+                if (visible(key)) {
+                    const int64_t diff = (int64_t)best - sc[i];
+                    const uint64_t e = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
+                    w = dn::softmax_weight(e, sum, inv_sum);
+                    wsum += w;
+                    if (w >= BIG_WEIGHT) {
+                        if (big[0] < 0) big[0] = (int32_t)key;
+                        else big[1] = (int32_t)key;
+                        w -= 65536;
+                    }
+                }
+                const uint32_t u = (uint32_t)(w + 0x8080);  // two digits, each biased by 0x80
+                b0 |= ((u & 0xff) ^ 0x80) << (8 * i);
+                b1 |= (((u >> 8) & 0xff) ^ 0x80) << (8 * i);
+            }
+            wd[0][t] = b0;
+            wd[1][t] = b1;
+        }
+        const v4i wf0 = v4i{(int)wd[0][0], (int)wd[0][1], (int)wd[0][2], (int)wd[0][3]};
+        const v4i wf1 = v4i{(int)wd[1][0], (int)wd[1][1], (int)wd[1][2], (int)wd[1][3]};
+        const int8_t* vb = vbase + (size_t)ks * DT * FRAG;
+#pragma unroll
+        for (uint32_t dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int b = 0; b < AP_V_PLANES; b++)
+                if (b < Lv) {
+                    const v4i vf = *(const v4i*)(vb + b * vl + dt * FRAG);
+                    pacc[dt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf0, vf, pacc[dt][b], 0, 0, 0);
+                    pacc[dt][b + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf1, vf, pacc[dt][b + 1], 0, 0, 0);
+                }
+    }
+    wsum += __shfl_xor(wsum, 16);
+    wsum += __shfl_xor(wsum, 32);
+
+    // Per query row: the residual goes to the first maximum; every large
+    // weight adds 65536 * v back.
+    if (lane < 16) {
+        sm.pre.info[wave][lane][0] = (int32_t)best_key;
+        sm.pre.info[wave][lane][1] = dn::sub_sat(dn::ONE_ACT, wsum);
+    }
+    sm.pre.big[wave][lane & 15][2 * grp] = big[0];
+    sm.pre.big[wave][lane & 15][2 * grp + 1] = big[1];
+    __syncthreads();
+
+    // Lane l of the value product holds dim l % 16 of each d-tile for query
+    // rows 4 * (l / 16) + i.
+    const int32_t* vcache = a.v_cache + (size_t)g * HD;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const uint32_t qq = 4 * grp + i, row = qt * 16 + qq;
+        if (row >= tokens) continue;
+        const uint32_t mkey = (uint32_t)sm.pre.info[wave][qq][0];
+        const int64_t resid = sm.pre.info[wave][qq][1];
+#pragma unroll
+        for (uint32_t dt = 0; dt < DT; dt++) {
+            const uint32_t dim = dt * 16 + (lane & 15);
+            uint64_t tot = 0;
+#pragma unroll
+            for (int s = 0; s < AP_V_PLANES + 1; s++) tot += (uint64_t)(int64_t)pacc[dt][s][i] << (8 * s);
+            tot += (uint64_t)(resid * vcache[(size_t)mkey * a.kv_stride + dim]);
+#pragma unroll
+            for (int j = 0; j < 8; j++) {
+                const int32_t bk = sm.pre.big[wave][qq][j];
+                if (bk >= 0) tot += (uint64_t)((int64_t)65536 * vcache[(size_t)bk * a.kv_stride + dim]);
+            }
+            a.ctx[(size_t)row * a.ctx_stride + (size_t)head * HD + dim] = dn::requantize((int64_t)tot);
+        }
+    }
+}
+
+template <uint32_t HD>
+int prefill_launch(const AttnArgs& a, uint32_t tokens, hipStream_t stream) {
+    const uint32_t QT = (tokens + 15) / 16;
+    hipLaunchKernelGGL(attn_q_planes_kernel<HD>, dim3(QT, a.heads), dim3(64), 0, stream, a, tokens);
+    hipLaunchKernelGGL(attn_kv_planes_kernel<HD>, dim3(a.planes.ks_cap, a.kv_heads), dim3(256), 0, stream, a, tokens);
+    const uint32_t wgs = QT * a.kv_heads * (a.heads / a.kv_heads / 4);
+    hipLaunchKernelGGL(attn_prefill_kernel<HD>, dim3(wgs), dim3(256), 0, stream, a, tokens);
+    return (int)hipGetLastError();
+}
+
+__global__ void softmax_terms_kernel(const uint32_t* diff, const uint64_t* e, const uint64_t* sum, uint32_t n,
+                                     uint64_t* e_out, int32_t* w_out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= n) return;
+    e_out[i] = dn::softmax_exp_diff(diff[i]);
+    w_out[i] = dn::softmax_weight(e[i], sum[i], 1.0 / (double)sum[i]);
+}
+
+}  // namespace
+
+int iris_softmax_terms(const uint32_t* d_diff, const uint64_t* d_e, const uint64_t* d_sum, uint32_t n,
+                       uint64_t* d_exp, int32_t* d_weight) {
+    if (n == 0) return 0;
+    if (!d_diff || !d_e || !d_sum || !d_exp || !d_weight) return IRIS_E_INVALID;
+    hipLaunchKernelGGL(softmax_terms_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, d_diff, d_e, d_sum, n,
+                       d_exp, d_weight);
+    hipError_t st = hipGetLastError();
+    if (st == hipSuccess) st = hipDeviceSynchronize();
+    return (int)st;
+}
+
+bool iris_attention_prefill_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys) {
+    const AttnPlanes& p = a.planes;
+    return tokens >= 2 && p.q && p.k && p.v && p.q_limbs && p.kv_limbs && (a.head_dim == 64 || a.head_dim == 128) &&
+           a.heads % a.kv_heads == 0 && (a.heads / a.kv_heads) % 4 == 0 && (tokens + 15) / 16 <= p.qt_cap &&
+           max_keys <= p.ks_cap * 64 && max_keys <= ATTN_MAX_KEYS;
+}
+
+int iris_attention_prefill_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream) {
+    if (!iris_attention_prefill_applies(a, tokens, max_keys)) return IRIS_E_INVALID;
+    return a.head_dim == 64 ? prefill_launch<64>(a, tokens, stream) : prefill_launch<128>(a, tokens, stream);
+}

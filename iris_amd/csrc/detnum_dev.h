@@ -242,6 +242,65 @@ __device__ inline int64_t softmax_exp_term(int64_t delta) {
     return 0;
 }
 
+// rte(x / c) for x >= 0: ops.rs:691-720 with a non-negative dividend.
+__device__ __forceinline__ uint64_t rte_div_small(uint64_t x, uint32_t c) {
+    uint64_t q = x / c;
+    const uint64_t twice = 2 * (x - q * c);
+    if (twice > c || (twice == c && (q & 1))) q++;
+    return q;
+}
+
+// acc_mul (ops.rs:685-689) of 0 <= a, b < 2^32: the product fits 64 bits.
+__device__ __forceinline__ uint64_t acc_mul_small(uint64_t a, uint64_t b) {
+    const uint64_t p = a * b;
+    uint64_t fl = p >> 32;
+    const uint64_t rem = p & 0xffffffffull;
+    if (rem > 0x80000000ull || (rem == 0x80000000ull && (fl & 1))) fl++;
+    return fl;
+}
+
+// softmax_exp_term (ops.rs:508-556) of delta = -(diff << 16), diff >= 0:
+// the only deltas the softmax forms (a logit minus the row's maximum).
+// diff >= 2^20 is at or below the -16 cut: zero. Below it r < ln 2 < 1 in
+// Q32.32, so every acc_mul multiplies two values under 2^32, none of the
+// saturating sums can saturate, and the divisions by 2, 6, 24 and 120 are of
+// non-negative values: the general routine's integers with 64-bit operations.
+__device__ __forceinline__ uint64_t softmax_exp_diff(uint32_t diff) {
+    if (diff >= (1u << 20)) return 0;
+    const uint64_t LN_2_BITS = 2977044472ull;
+    const uint64_t positive = (uint64_t)diff << 16;
+    const uint64_t shift = positive / LN_2_BITS;
+    const uint64_t r = positive - shift * LN_2_BITS;
+    const uint64_t r2 = acc_mul_small(r, r), r3 = acc_mul_small(r2, r);
+    const uint64_t r4 = acc_mul_small(r3, r), r5 = acc_mul_small(r4, r);
+    const int64_t approx = (int64_t)ONE_ACC - (int64_t)r + (int64_t)rte_div_small(r2, 2) -
+                           (int64_t)rte_div_small(r3, 6) + (int64_t)rte_div_small(r4, 24) -
+                           (int64_t)rte_div_small(r5, 120);
+    if (approx <= 0) return 0;
+    return (uint64_t)rshift_rte(approx, (uint32_t)shift);
+}
+
+// attention_softmax_raw_weight (ops.rs:269-271), requantize(div_acc(e, sum)),
+// for 0 <= e <= 2^32 <= sum < 2^62 and inv_sum = 1.0 / sum: the quotient
+// (e << 32) / sum from a double estimate (off by at most one), made exact by
+// the integer remainder (exact modulo 2^64, and |remainder| < 2 * sum), then
+// rounded half to even as div_acc does, then requantized.
+__device__ __forceinline__ int32_t softmax_weight(uint64_t e, uint64_t sum, double inv_sum) {
+    uint64_t q = (uint64_t)((double)e * 4294967296.0 * inv_sum);
+    int64_t rem = (int64_t)((e << 32) - q * sum);
+    while (rem < 0) {
+        q--;
+        rem += (int64_t)sum;
+    }
+    while ((uint64_t)rem >= sum) {
+        q++;
+        rem -= (int64_t)sum;
+    }
+    const uint64_t other = sum - (uint64_t)rem;
+    if ((uint64_t)rem > other || ((uint64_t)rem == other && (q & 1))) q++;
+    return requantize((int64_t)q);
+}
+
 // ops.rs:357-377
 __device__ inline int32_t tanh_act(int32_t x) {
     const int32_t LIN = 27 << 16, QUAD = 9 << 16, SAT = 3 << 16;

@@ -6,6 +6,28 @@
 constexpr uint32_t ATTN_MAX_KEYS = 4096;      // visible keys one query attends to
 constexpr uint32_t ATTN_MAX_HEAD_DIM = 256;
 
+// Work space of the multi-row attention: the signed byte digits (four
+// planes) of the queries, keys and values in MFMA operand tiles, and the
+// digits each tile needs (5 = a value beyond four digits: scalar path).
+struct AttnPlanes {
+    int8_t* q;               // [4][heads][qt_cap][head_dim/64][1 KB]
+    int8_t* k;               // [4][kv_heads][ks_cap*4][head_dim/64][1 KB]
+    int8_t* v;               // [4][kv_heads][ks_cap][head_dim/16][1 KB]
+    uint8_t* q_limbs;        // [heads][qt_cap]
+    uint8_t* kv_limbs;       // [kv_heads][ks_cap][2]: keys', values' digits per 64-key step
+    uint32_t qt_cap;         // 16-row query tiles
+    uint32_t ks_cap;         // 64-key steps
+};
+
+// Bytes of each plane buffer for heads x head_dim queries over qt_cap tiles
+// and kv_heads x head_dim keys over ks_cap steps.
+inline uint64_t attn_q_planes_bytes(uint32_t heads, uint32_t head_dim, uint32_t qt_cap) {
+    return 4ull * heads * qt_cap * 16 * head_dim;
+}
+inline uint64_t attn_kv_planes_bytes(uint32_t kv_heads, uint32_t head_dim, uint32_t ks_cap) {
+    return 4ull * kv_heads * ks_cap * 64 * head_dim;
+}
+
 struct AttnArgs {
     const int32_t* q;        // [tokens][heads*head_dim]
     uint32_t q_stride;
@@ -27,6 +49,9 @@ struct AttnArgs {
     int64_t* chunk_acc;      // [heads][ATTN_MAX_CHUNKS][head_dim]
     int32_t* chunk_wsum;     // [heads][ATTN_MAX_CHUNKS]
     int32_t* max_weight;     // [heads]: the first maximum's weight before the residual
+    // Digit planes for the multi-row MFMA path (planes.q null: the scalar
+    // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes.
+    AttnPlanes planes;
 };
 
 constexpr uint32_t ATTN_CHUNK = 128;  // keys per workgroup in the split decode path
@@ -35,6 +60,11 @@ constexpr uint32_t ATTN_MAX_CHUNKS = ATTN_MAX_KEYS / ATTN_CHUNK;
 // Attention for `tokens` query rows; max_keys bounds the visible keys of the
 // last row (checked against the kernel's capacity).
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
+// The multi-row MFMA attention (attn_prefill.hip): applies to head sizes 64
+// and 128 with four or a multiple of four query heads per KV head, given
+// plane space for `tokens` rows and `max_keys` keys.
+bool iris_attention_prefill_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys);
+int iris_attention_prefill_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
 int iris_embed_rows_launch(const int32_t* d_ids, uint32_t count, const uint8_t* embed_raw, uint32_t row_bytes,
                            uint32_t hidden, int32_t scale, int32_t* out, hipStream_t stream);
 

@@ -441,6 +441,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         a.chunk_acc = s->attn_chunk_acc;
         a.chunk_wsum = s->attn_chunk_wsum;
         a.max_weight = s->attn_max_weight;
+        a.planes = s->attn_planes;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 3. attended = W_o ctx + x.
         g = GemvArgs{};
@@ -578,6 +579,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
         a.chunk_acc = s->attn_chunk_acc;
         a.chunk_wsum = s->attn_chunk_wsum;
         a.max_weight = s->attn_max_weight;
+        a.planes = s->attn_planes;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 4. attended = rms_norm(W_o ctx, post_attention) + x  (:879-892)
         g = GemvArgs{};
@@ -761,6 +763,17 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
         size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
         if (st == hipSuccess) st = hipMalloc((void**)&s->planes, gemm_planes_bytes((uint32_t)widest, max_rows));
         alloc(&s->token_limbs, max_rows);
+        AttnPlanes& ap = s->attn_planes;
+        ap.qt_cap = (max_rows + 15) / 16;
+        ap.ks_cap = (max_positions + 63) / 64;
+        auto alloc8 = [&](void** p, uint64_t bytes) {
+            if (st == hipSuccess) st = hipMalloc(p, bytes);
+        };
+        alloc8((void**)&ap.q, attn_q_planes_bytes(d.heads, m->max_head_dim, ap.qt_cap));
+        alloc8((void**)&ap.k, attn_kv_planes_bytes(d.kv_heads, m->max_head_dim, ap.ks_cap));
+        alloc8((void**)&ap.v, attn_kv_planes_bytes(d.kv_heads, m->max_head_dim, ap.ks_cap));
+        alloc8((void**)&ap.q_limbs, (uint64_t)d.heads * ap.qt_cap);
+        alloc8((void**)&ap.kv_limbs, 2ull * d.kv_heads * ap.ks_cap);
     }
     if (d.family == IRIS_FAMILY_GEMMA_DENSE) {
         const size_t lp = (size_t)d.layers * d.ple_width;
@@ -807,6 +820,11 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->attn_chunk_acc);
     hipFree(s->attn_chunk_wsum);
     hipFree(s->attn_max_weight);
+    hipFree(s->attn_planes.q);
+    hipFree(s->attn_planes.k);
+    hipFree(s->attn_planes.v);
+    hipFree(s->attn_planes.q_limbs);
+    hipFree(s->attn_planes.kv_limbs);
     if (s->stream) hipStreamDestroy(s->stream);
     delete s;
 }

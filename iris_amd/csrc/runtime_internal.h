@@ -5,6 +5,7 @@
 #include <string>
 #include <vector>
 
+#include "layer_kernels.h"
 #include "q8_internal.h"
 
 struct HostTensor {
@@ -84,6 +85,8 @@ struct IrisSession {
     int64_t* attn_chunk_acc = nullptr;
     int32_t* attn_chunk_wsum = nullptr;
     int32_t* attn_max_weight = nullptr;
+    // multi-row attention digit planes (null for single-row sessions)
+    AttnPlanes attn_planes{};
     hipGraphExec_t graph_exec = nullptr;
     bool graph_keep_logits = false;
 };

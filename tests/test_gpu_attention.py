@@ -1,0 +1,103 @@
+"""GPU parity of the multi-row attention on the int8 matrix cores.
+
+The narrow softmax routines are checked against the oracle's general ones
+over every logit difference that can give a non-zero exp term and over
+weight quotients chosen to hit each rounding case; the kernel itself
+through teacher-forced passes of models with head sizes 64 and 128 (rows
+across several 64-key steps and partial 16-row tiles), a Gemma model with
+sliding windows, and a layer whose values need a fourth digit (the
+workgroups take the scalar one-row routine there).
+"""
+import hashlib
+
+import numpy as np
+import pytest
+
+from iris_amd import native, synth
+from iris_amd.direct import DeviceModel, Session
+from oracle import cpu
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def device():
+    native.check(native.lib().q8gpu_init(), "q8gpu_init")
+
+
+def _softmax_terms(diff, e, s):
+    n = diff.size
+    L = native.lib()
+    dd, de, ds = (native.DeviceBuffer.from_array(np.ascontiguousarray(a)) for a in (diff, e, s))
+    dexp, dw = native.DeviceBuffer(8 * n), native.DeviceBuffer(4 * n)
+    native.check(L.iris_softmax_terms(dd.ptr, de.ptr, ds.ptr, n, dexp.ptr, dw.ptr), "softmax terms")
+    return dexp.to_array(np.uint64, (n,)), dw.to_array(np.int32, (n,))
+
+
+def test_softmax_terms_against_oracle():
+    O = cpu.lib()
+    # Every logit difference below the -16 cut, and a few at and past it.
+    diff = np.arange(0, (1 << 20) + 8, dtype=np.uint32)
+    diff = np.concatenate([diff, np.array([1 << 24, 1 << 31, 2 ** 32 - 1], np.uint32)])
+    # Raw weights: e in [0, 2^32] against sums in [2^32, 4096 * 2^32), and
+    # sums k * 2^32 with e = k/2 + j*k (k even): quotients ending in exactly
+    # one half, so the ties-to-even step of div_acc is taken both ways.
+    rng = np.random.default_rng(3)
+    n = diff.size
+    sums = rng.integers(1 << 32, 4096 << 32, n, dtype=np.uint64)
+    es = rng.integers(0, (1 << 32) + 1, n, dtype=np.uint64)
+    k = 2 * rng.integers(1, 2048, n // 4, dtype=np.uint64)
+    sums[: n // 4] = k << np.uint64(32)
+    es[: n // 4] = np.minimum(k // np.uint64(2) + k * rng.integers(0, 1 << 20, n // 4, dtype=np.uint64),
+                              np.uint64(1 << 32))
+    es[:3] = [0, 1 << 32, 1 << 32]
+    sums[:3] = [1 << 32, 1 << 32, (1 << 33) + 2]
+    got_e, got_w = _softmax_terms(diff, es, sums)
+    want_e = np.array([O.dn_softmax_exp_term(-(int(d) << 16)) for d in diff], np.int64).astype(np.uint64)
+    assert np.array_equal(got_e, want_e)
+    want_w = np.array([O.dn_requantize(O.dn_div_acc(int(e), int(s))) for e, s in zip(es, sums)], np.int32)
+    assert np.array_equal(got_w, want_w)
+
+
+def _check_pass(m, rows, max_positions=None):
+    ids = synth.token_ids(11, rows, m.vocab)
+    dm = DeviceModel(m)
+    s = Session(dm, max_positions or rows, rows)
+    got, hashes = s.layer_pass(ids)
+    r = cpu.OracleRun(m, max_positions or rows)
+    _, layers = r.pass_rows(list(ids), 0, keep_layers=True)
+    for layer in range(m.num_layers):
+        assert np.array_equal(got[layer], layers[layer]), layer
+        assert hashes[layer] == hashlib.sha256(layers[layer].astype("<i4").tobytes()).hexdigest()
+    s.free()
+    dm.free()
+
+
+@pytest.mark.parametrize("head_dim,heads,kv_heads,rows", [(128, 8, 2, 150), (64, 16, 2, 77), (128, 4, 1, 17)])
+def test_prefill_attention_mistral(head_dim, heads, kv_heads, rows):
+    # GQA groups of four and eight, 1..3 key steps, partial query tiles.
+    m = synth.mistral_model(512, 2, heads, kv_heads, head_dim, 512, 512, seed=31 + head_dim + rows)
+    _check_pass(m, rows, max_positions=rows + 40)
+
+
+def test_prefill_attention_large_values_take_the_scalar_routine():
+    # Layer 0's attention norm weights scaled by 512: its values need four
+    # digits, so its workgroups use the one-row routine; layer 1 stays on the
+    # matrix cores.
+    m = synth.mistral_model(512, 2, 8, 2, 64, 512, 512, seed=77)
+    key = synth.PREFIX + "layers.0.input_layernorm.weight"
+    m.tensors[key] = (m.tensors[key].astype(np.int64) * 512).clip(-2 ** 31, 2 ** 31 - 1).astype(np.int32)
+    _check_pass(m, 70)
+
+
+def test_prefill_attention_gemma_sliding_window():
+    # Four query heads on one KV head; sliding layers of head size 64 with a
+    # 40-key window (the first visible key moves inside the 64-key steps)
+    # alternating with full layers of head size 128 and half rotary, the last
+    # two layers reading earlier layers' caches.
+    shape = synth.gemma_shape(256, 4, 4, 1, 64, 1024, 64, global_head_dim=128, sliding_window=40,
+                              layer_types=["sliding_attention", "full_attention"] * 2, num_kv_shared_layers=2,
+                              partial_rotary=0.5, softcap=30.0)
+    m = synth.gemma_model(shape, 512, seed=5)
+    _check_pass(m, 100)
+    _check_pass(synth.tiny_gemma(), 33)

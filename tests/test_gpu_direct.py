@@ -71,9 +71,9 @@ def test_teacher_forced_layer_pass_matches_oracle():
 
 
 def test_mistral_7b_shape_generation_matches_oracle():
-    # BASELINE configuration 4's shape (32 layers, hidden 4096, GQA 32/8,
-    # SwiGLU 14336, vocab 32000): a short prompt and three selections, every
-    # logit compared with the oracle.
+    # The Mistral-7B shape (32 layers, hidden 4096, GQA 32/8, SwiGLU 14336,
+    # vocab 32000): a short prompt and three selections, every logit
+    # compared with the oracle.
     m = synth.mistral_7b(seed=0x7B7B)
     prompt = synth.token_ids(7, 4, 32000)
     print("mistral-7b shape: uploading", flush=True)

@@ -124,7 +124,7 @@ def test_no_tokens_and_width_mismatch():
 
 @pytest.mark.parametrize("per_row_scale", [True, False])
 def test_microbench_gemv_full_size(per_row_scale):
-    # BASELINE configuration 2, GEMV case: M=1, K=4096, N=14336, every output.
+    # The microbenchmark GEMV: M=1, K=4096, N=14336, every output.
     N, K = 14336, 4096
     raw = synth.q8_matrix(synth.tensor_seed(2, 1), N, K, synth.scale_base_for(K), per_row_scale)
     rng = np.random.default_rng(2)
@@ -136,7 +136,7 @@ def test_microbench_gemv_full_size(per_row_scale):
 
 
 def test_microbench_gemm_full_size_sampled_rows():
-    # BASELINE configuration 2, GEMM case: M=512, K=N=4096; every token of
+    # The microbenchmark GEMM: M=512, K=N=4096; every token of
     # 96 sampled rows against the oracle, plus the stress (full-range) set.
     N, K, M = 4096, 4096, 512
     raw = synth.q8_matrix(synth.tensor_seed(2, 2), N, K, synth.scale_base_for(K), True)
