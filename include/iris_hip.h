@@ -198,15 +198,18 @@ int iris_session_time_decode(IrisSession* session, const int32_t* prompt, uint32
  * on the session's stream. */
 int iris_session_time_pass(IrisSession* session, const int32_t* ids, uint32_t count, double* ms);
 
-/* Numerics check of the multi-row attention's softmax routines, run on the
+/* Numerics check of the attention kernels' narrow routines, run on the
  * device over n inputs (device pointers; synchronous): exp_out[i] is the
  * softmax exp term of a logit diff[i] below its row maximum, weight_out[i]
  * the raw weight requantize(div_acc(e[i], sum[i])) for e[i] <= 2^32 <=
- * sum[i]. No counterpart in the reference: it compares these narrow
- * routines with the reference's attention_softmax_exp_term and
- * attention_softmax_raw_weight (crates/det-num/src/ops.rs:264-271). */
-int iris_softmax_terms(const uint32_t* diff, const uint64_t* e, const uint64_t* sum, uint32_t n,
-                       uint64_t* exp_out, int32_t* weight_out);
+ * sum[i], score_out[i] the scaled score of the wrapping dot product dot[i].
+ * No counterpart in the reference: it compares these routines with the
+ * reference's attention_softmax_exp_term and attention_softmax_raw_weight
+ * (crates/det-num/src/ops.rs:264-271) and scaled_score
+ * (crates/det-num/src/mistral.rs:130-145). */
+int iris_attention_numerics(const uint32_t* diff, const uint64_t* e, const uint64_t* sum, const int64_t* dot,
+                            uint32_t scale_q32, uint32_t n, uint64_t* exp_out, int32_t* weight_out,
+                            int32_t* score_out);
 
 /* SHA-256 (FIPS 180-4) of `len` bytes into out[32]; the hash
  * iris_session_layer_pass uses. Host code only. */

@@ -173,106 +173,91 @@ struct PrefillSmem {
     int32_t big[4][16][8];    // per wave and query row: large-weight keys (two per lane group, -1 none)
 };
 
-// The scores of one 16-key tile against the wave's 16 query rows: lane l
-// holds query l % 16 and keys 4 * (l / 16) + i of the tile.
-template <uint32_t HD>
-__device__ __forceinline__ void tile_scores(const AttnArgs& a, const int8_t* kb, size_t kl, int Lk, int Lq,
-                                            const v4i (&qf)[AP_PLANES][HD / 64], int32_t (&sc)[4]) {
-    constexpr uint32_t DS = HD / 64;
-    v4i acc[2 * AP_PLANES - 1];
+template <uint32_t HD, int LQK>
+__device__ __forceinline__ void load_key_tile(const int8_t* kb, size_t kl, v4i (&kf)[LQK][HD / 64]) {
 #pragma unroll
-    for (int s = 0; s < 2 * AP_PLANES - 1; s++) acc[s] = v4i{0, 0, 0, 0};
+    for (int l = 0; l < LQK; l++)
 #pragma unroll
-    for (int l = 0; l < AP_PLANES; l++) {
-        if (l < Lk) {
+        for (uint32_t ds = 0; ds < HD / 64; ds++) kf[l][ds] = *(const v4i*)(kb + l * kl + ds * FRAG);
+}
+
+// The scores of one 16-key tile against the wave's 16 query rows, from LQK
+// digit planes of each: lane l holds query l % 16 and keys 4 * (l / 16) + i
+// of the tile.
+template <uint32_t HD, int LQK>
+__device__ __forceinline__ void tile_scores(const AttnArgs& a, const v4i (&kf)[LQK][HD / 64],
+                                            const v4i (&qf)[LQK][HD / 64], int32_t (&sc)[4]) {
+    constexpr int NS = 2 * LQK - 1;
+    v4i acc[NS];
 #pragma unroll
-            for (uint32_t ds = 0; ds < DS; ds++) {
-                const v4i kf = *(const v4i*)(kb + l * kl + ds * FRAG);
+    for (int s = 0; s < NS; s++) acc[s] = v4i{0, 0, 0, 0};
 #pragma unroll
-                for (int b = 0; b < AP_PLANES; b++)
-                    if (b < Lq) acc[l + b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf, qf[b][ds], acc[l + b], 0, 0, 0);
-            }
-        }
-    }
+    for (uint32_t ds = 0; ds < HD / 64; ds++)
+#pragma unroll
+        for (int l = 0; l < LQK; l++)
+#pragma unroll
+            for (int b = 0; b < LQK; b++)
+                acc[l + b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kf[l][ds], qf[b][ds], acc[l + b], 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
         uint64_t s = 0;  // the wrapping i64 dot product
 #pragma unroll
-        for (int j = 0; j < 2 * AP_PLANES - 1; j++) s += (uint64_t)(int64_t)acc[j][i] << (8 * j);
+        for (int j = 0; j < NS; j++) s += (uint64_t)(int64_t)acc[j][i] << (8 * j);
         sc[i] = a.scaled ? dn::scaled_score_from_sum((int64_t)s, a.scale_q32) : dn::requantize((int64_t)s);
     }
 }
 
-template <uint32_t HD>
-__global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
+// One wave: 16 query rows of one head over key steps [ks0, ks1), queries
+// and keys of LQK digits, values of AP_V_PLANES.
+template <uint32_t HD, int LQK>
+__device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens, PrefillSmem& sm, uint32_t g,
+                                             uint32_t head, uint32_t qt, uint32_t ks0, uint32_t ks1) {
     constexpr uint32_t DS = HD / 64, DT = HD / 16;
-    __shared__ union {
-        AttnRowSmem row;
-        PrefillSmem pre;
-    } sm;
-    __shared__ int s_scalar;
     const AttnPlanes& p = a.planes;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t group = a.heads / a.kv_heads, hblocks = group / 4, per_qt = a.kv_heads * hblocks;
-    const uint32_t QT = (tokens + 15) / 16;
-    const uint32_t qt = QT - 1 - blockIdx.x / per_qt;  // the longest rows first
-    const uint32_t rest = blockIdx.x % per_qt, g = rest / hblocks, h0 = g * group + (rest % hblocks) * 4;
-    const uint32_t head = h0 + wave;
     const uint32_t pos0 = (uint32_t)(*a.d_pos);
-    const uint32_t rows = min(16u, tokens - qt * 16);
-    const uint32_t first_pos = pos0 + qt * 16, last_pos = first_pos + rows - 1;
-    const uint32_t first_key = (a.window == 0 || first_pos + 1 <= a.window) ? 0 : first_pos + 1 - a.window;
-    const uint32_t ks0 = first_key / 64, ks1 = last_pos / 64 + 1;
-    const uint8_t* kvl = p.kv_limbs + (size_t)g * p.ks_cap * 2;
-
-    if (tid == 0) s_scalar = 0;
-    __syncthreads();
-    if (tid < 4 && p.q_limbs[(h0 + tid) * p.qt_cap + qt] > AP_PLANES) s_scalar = 1;
-    for (uint32_t ks = ks0 + tid; ks < ks1; ks += 256)
-        if (kvl[2 * ks] > AP_PLANES || kvl[2 * ks + 1] > AP_V_PLANES) s_scalar = 1;
-    __syncthreads();
-    if (s_scalar) {
-        for (uint32_t i = 0; i < 4 * rows; i++) attend_row(a, h0 + i / rows, qt * 16 + i % rows, sm.row);
-        return;
-    }
 
     // This lane's query row for the scores, and its visible keys.
     const uint32_t qrow = qt * 16 + (lane & 15), grp = lane >> 4;
     const bool qvalid = qrow < tokens;
     const uint32_t qpos = pos0 + qrow;
     const uint32_t qstart = (a.window == 0 || qpos + 1 <= a.window) ? 0 : qpos + 1 - a.window;
-    const int Lq = p.q_limbs[head * p.qt_cap + qt];
-    v4i qf[AP_PLANES][DS];
+    auto visible = [&](uint32_t key) { return qvalid && key >= qstart && key <= qpos; };
+    v4i qf[LQK][DS];
     {
         const int8_t* qb = p.q + ((size_t)head * p.qt_cap + qt) * DS * FRAG + lane * 16;
         const size_t ql = (size_t)a.heads * p.qt_cap * DS * FRAG;
 #pragma unroll
-        for (int b = 0; b < AP_PLANES; b++)
+        for (int b = 0; b < LQK; b++)
 #pragma unroll
             for (uint32_t ds = 0; ds < DS; ds++) qf[b][ds] = *(const v4i*)(qb + b * ql + ds * FRAG);
     }
     const size_t kl = (size_t)a.kv_heads * p.ks_cap * 4 * DS * FRAG;
     const int8_t* kbase = p.k + (size_t)g * p.ks_cap * 4 * DS * FRAG + lane * 16;
-    auto visible = [&](uint32_t key) { return qvalid && key >= qstart && key <= qpos; };
+    const uint32_t kt0 = ks0 * 4, kt1 = ks1 * 4;  // 16-key tiles
+    v4i kf[LQK][DS], kn[LQK][DS];
 
     // (1) the first maximum: keys run in increasing order in each lane.
     int32_t best = INT32_MIN;
     uint32_t best_key = 0xffffffffu;
-    for (uint32_t ks = ks0; ks < ks1; ks++) {
-        const int Lk = kvl[2 * ks];
+    load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+#pragma unroll 1
+    for (uint32_t kt = kt0; kt < kt1; kt++) {
+        if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
+        int32_t sc[4];
+        tile_scores<HD, LQK>(a, kf, qf, sc);
 #pragma unroll
-        for (uint32_t t = 0; t < 4; t++) {
-            int32_t sc[4];
-            tile_scores<HD>(a, kbase + (size_t)(ks * 4 + t) * DS * FRAG, kl, Lk, Lq, qf, sc);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t key = ks * 64 + 16 * t + 4 * grp + i;
-                if (visible(key) && sc[i] > best) {
-                    best = sc[i];
-                    best_key = key;
-                }
+        for (int i = 0; i < 4; i++) {
+            const uint32_t key = kt * 16 + 4 * grp + i;
+            if (visible(key) && sc[i] > best) {
+                best = sc[i];
+                best_key = key;
             }
         }
+#pragma unroll
+        for (int l = 0; l < LQK; l++)
+#pragma unroll
+            for (uint32_t ds = 0; ds < DS; ds++) kf[l][ds] = kn[l][ds];
     }
 #pragma unroll
     for (int off = 16; off <= 32; off <<= 1) {
@@ -286,22 +271,26 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, 
 
     // (2) the sum of exp terms (non-negative, so no order and no saturation).
     uint64_t sum = 0;
-    for (uint32_t ks = ks0; ks < ks1; ks++) {
-        const int Lk = kvl[2 * ks];
+    load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+#pragma unroll 1
+    for (uint32_t kt = kt0; kt < kt1; kt++) {
+        if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
+        int32_t sc[4];
+        tile_scores<HD, LQK>(a, kf, qf, sc);
 #pragma unroll
-        for (uint32_t t = 0; t < 4; t++) {
-            int32_t sc[4];
-            tile_scores<HD>(a, kbase + (size_t)(ks * 4 + t) * DS * FRAG, kl, Lk, Lq, qf, sc);
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                const uint32_t key = ks * 64 + 16 * t + 4 * grp + i;
-                if (visible(key)) sum += dn::softmax_exp_diff((uint32_t)((int64_t)best - sc[i] > (1 << 20) ? (1 << 20) : (int64_t)best - sc[i]));
-            }
+        for (int i = 0; i < 4; i++) {
+            const uint32_t key = kt * 16 + 4 * grp + i;
+            const int64_t diff = (int64_t)best - sc[i];
+            if (visible(key)) sum += dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
         }
+#pragma unroll
+        for (int l = 0; l < LQK; l++)
+#pragma unroll
+            for (uint32_t ds = 0; ds < DS; ds++) kf[l][ds] = kn[l][ds];
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
-    const double inv_sum = qvalid ? 1.0 / (double)sum : 0.0;
+    const double q_scale = qvalid ? 4294967296.0 / (double)sum : 0.0;
 
     // (3) weights, their sum, and the weighted values.
     v4i pacc[DT][AP_V_PLANES + 1];
@@ -313,22 +302,34 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, 
     const int8_t* vbase = p.v + (size_t)g * p.ks_cap * DT * FRAG + lane * 16;
     int32_t wsum = 0;
     int32_t big[2] = {-1, -1};
+    load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+#pragma unroll 1
     for (uint32_t ks = ks0; ks < ks1; ks++) {
-        const int Lk = kvl[2 * ks], Lv = kvl[2 * ks + 1];
-        uint32_t wd[2][4];  // the two weight digits of this lane's 16 keys, byte 4t + i
+        // The step's value operands, needed after its four score tiles.
+        v4i vf[DT][AP_V_PLANES];
+        const int8_t* vb = vbase + (size_t)ks * DT * FRAG;
 #pragma unroll
+        for (uint32_t dt = 0; dt < DT; dt++)
+#pragma unroll
+            for (int b = 0; b < AP_V_PLANES; b++) vf[dt][b] = *(const v4i*)(vb + b * vl + dt * FRAG);
+        // The two weight digits of this lane's 16 keys: byte 4t + i of wf0/wf1
+        // (tile t is shifted in as the last component).
+        v4i wf0 = v4i{0, 0, 0, 0}, wf1 = v4i{0, 0, 0, 0};
+#pragma unroll 1
         for (uint32_t t = 0; t < 4; t++) {
+            const uint32_t kt = ks * 4 + t;
+            if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
             int32_t sc[4];
-            tile_scores<HD>(a, kbase + (size_t)(ks * 4 + t) * DS * FRAG, kl, Lk, Lq, qf, sc);
+            tile_scores<HD, LQK>(a, kf, qf, sc);
             uint32_t b0 = 0, b1 = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t key = ks * 64 + 16 * t + 4 * grp + i;
+                const uint32_t key = kt * 16 + 4 * grp + i;
                 int32_t w = 0;
                 if (visible(key)) {
                     const int64_t diff = (int64_t)best - sc[i];
                     const uint64_t e = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
-                    w = dn::softmax_weight(e, sum, inv_sum);
+                    w = dn::softmax_weight(e, sum, q_scale);
                     wsum += w;
                     if (w >= BIG_WEIGHT) {
                         if (big[0] < 0) big[0] = (int32_t)key;
@@ -340,21 +341,20 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, 
                 b0 |= ((u & 0xff) ^ 0x80) << (8 * i);
                 b1 |= (((u >> 8) & 0xff) ^ 0x80) << (8 * i);
             }
-            wd[0][t] = b0;
-            wd[1][t] = b1;
+            wf0 = v4i{wf0[1], wf0[2], wf0[3], (int)b0};
+            wf1 = v4i{wf1[1], wf1[2], wf1[3], (int)b1};
+#pragma unroll
+            for (int l = 0; l < LQK; l++)
+#pragma unroll
+                for (uint32_t ds = 0; ds < DS; ds++) kf[l][ds] = kn[l][ds];
         }
-        const v4i wf0 = v4i{(int)wd[0][0], (int)wd[0][1], (int)wd[0][2], (int)wd[0][3]};
-        const v4i wf1 = v4i{(int)wd[1][0], (int)wd[1][1], (int)wd[1][2], (int)wd[1][3]};
-        const int8_t* vb = vbase + (size_t)ks * DT * FRAG;
 #pragma unroll
         for (uint32_t dt = 0; dt < DT; dt++)
 #pragma unroll
-            for (int b = 0; b < AP_V_PLANES; b++)
-                if (b < Lv) {
-                    const v4i vf = *(const v4i*)(vb + b * vl + dt * FRAG);
-                    pacc[dt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf0, vf, pacc[dt][b], 0, 0, 0);
-                    pacc[dt][b + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf1, vf, pacc[dt][b + 1], 0, 0, 0);
-                }
+            for (int b = 0; b < AP_V_PLANES; b++) {
+                pacc[dt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf0, vf[dt][b], pacc[dt][b], 0, 0, 0);
+                pacc[dt][b + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf1, vf[dt][b], pacc[dt][b + 1], 0, 0, 0);
+            }
     }
     wsum += __shfl_xor(wsum, 16);
     wsum += __shfl_xor(wsum, 32);
@@ -362,11 +362,11 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, 
     // Per query row: the residual goes to the first maximum; every large
     // weight adds 65536 * v back.
     if (lane < 16) {
-        sm.pre.info[wave][lane][0] = (int32_t)best_key;
-        sm.pre.info[wave][lane][1] = dn::sub_sat(dn::ONE_ACT, wsum);
+        sm.info[wave][lane][0] = (int32_t)best_key;
+        sm.info[wave][lane][1] = dn::sub_sat(dn::ONE_ACT, wsum);
     }
-    sm.pre.big[wave][lane & 15][2 * grp] = big[0];
-    sm.pre.big[wave][lane & 15][2 * grp + 1] = big[1];
+    sm.big[wave][lane & 15][2 * grp] = big[0];
+    sm.big[wave][lane & 15][2 * grp + 1] = big[1];
     __syncthreads();
 
     // Lane l of the value product holds dim l % 16 of each d-tile for query
@@ -376,8 +376,8 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, 
     for (int i = 0; i < 4; i++) {
         const uint32_t qq = 4 * grp + i, row = qt * 16 + qq;
         if (row >= tokens) continue;
-        const uint32_t mkey = (uint32_t)sm.pre.info[wave][qq][0];
-        const int64_t resid = sm.pre.info[wave][qq][1];
+        const uint32_t mkey = (uint32_t)sm.info[wave][qq][0];
+        const int64_t resid = sm.info[wave][qq][1];
 #pragma unroll
         for (uint32_t dt = 0; dt < DT; dt++) {
             const uint32_t dim = dt * 16 + (lane & 15);
@@ -387,11 +387,49 @@ __global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, 
             tot += (uint64_t)(resid * vcache[(size_t)mkey * a.kv_stride + dim]);
 #pragma unroll
             for (int j = 0; j < 8; j++) {
-                const int32_t bk = sm.pre.big[wave][qq][j];
+                const int32_t bk = sm.big[wave][qq][j];
                 if (bk >= 0) tot += (uint64_t)((int64_t)65536 * vcache[(size_t)bk * a.kv_stride + dim]);
             }
             a.ctx[(size_t)row * a.ctx_stride + (size_t)head * HD + dim] = dn::requantize((int64_t)tot);
         }
+    }
+}
+
+template <uint32_t HD>
+__global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
+    __shared__ union {
+        AttnRowSmem row;
+        PrefillSmem pre;
+    } sm;
+    __shared__ int s_limbs;
+    const AttnPlanes& p = a.planes;
+    const uint32_t tid = threadIdx.x, wave = tid >> 6;
+    const uint32_t group = a.heads / a.kv_heads, hblocks = group / 4, per_qt = a.kv_heads * hblocks;
+    const uint32_t QT = (tokens + 15) / 16;
+    const uint32_t qt = QT - 1 - blockIdx.x / per_qt;  // the longest rows first
+    const uint32_t rest = blockIdx.x % per_qt, g = rest / hblocks, h0 = g * group + (rest % hblocks) * 4;
+    const uint32_t pos0 = (uint32_t)(*a.d_pos);
+    const uint32_t rows = min(16u, tokens - qt * 16);
+    const uint32_t first_pos = pos0 + qt * 16, last_pos = first_pos + rows - 1;
+    const uint32_t first_key = (a.window == 0 || first_pos + 1 <= a.window) ? 0 : first_pos + 1 - a.window;
+    const uint32_t ks0 = first_key / 64, ks1 = last_pos / 64 + 1;
+    const uint8_t* kvl = p.kv_limbs + (size_t)g * p.ks_cap * 2;
+
+    // Digits the block's queries and keys need (values: at most three);
+    // 5 or more sends the block to the one-row routine.
+    if (tid == 0) s_limbs = 1;
+    __syncthreads();
+    if (tid < 4) atomicMax(&s_limbs, (int)p.q_limbs[(h0 + tid) * p.qt_cap + qt]);
+    for (uint32_t ks = ks0 + tid; ks < ks1; ks += 256)
+        atomicMax(&s_limbs, kvl[2 * ks + 1] > AP_V_PLANES ? AP_PLANES + 1 : (int)kvl[2 * ks]);
+    __syncthreads();
+    const int limbs = s_limbs;
+    if (limbs > AP_PLANES) {
+        for (uint32_t i = 0; i < 4 * rows; i++) attend_row(a, h0 + i / rows, qt * 16 + i % rows, sm.row);
+    } else if (limbs <= 3) {
+        prefill_wave<HD, 3>(a, tokens, sm.pre, g, h0 + wave, qt, ks0, ks1);
+    } else {
+        prefill_wave<HD, 4>(a, tokens, sm.pre, g, h0 + wave, qt, ks0, ks1);
     }
 }
 
@@ -405,22 +443,24 @@ int prefill_launch(const AttnArgs& a, uint32_t tokens, hipStream_t stream) {
     return (int)hipGetLastError();
 }
 
-__global__ void softmax_terms_kernel(const uint32_t* diff, const uint64_t* e, const uint64_t* sum, uint32_t n,
-                                     uint64_t* e_out, int32_t* w_out) {
+__global__ void attention_numerics_kernel(const uint32_t* diff, const uint64_t* e, const uint64_t* sum,
+                                          const int64_t* dot, uint32_t scale_q32, uint32_t n, uint64_t* e_out,
+                                          int32_t* w_out, int32_t* score_out) {
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     e_out[i] = dn::softmax_exp_diff(diff[i]);
-    w_out[i] = dn::softmax_weight(e[i], sum[i], 1.0 / (double)sum[i]);
+    w_out[i] = dn::softmax_weight(e[i], sum[i], 4294967296.0 / (double)sum[i]);
+    score_out[i] = dn::scaled_score_from_sum(dot[i], scale_q32);
 }
 
 }  // namespace
 
-int iris_softmax_terms(const uint32_t* d_diff, const uint64_t* d_e, const uint64_t* d_sum, uint32_t n,
-                       uint64_t* d_exp, int32_t* d_weight) {
+int iris_attention_numerics(const uint32_t* d_diff, const uint64_t* d_e, const uint64_t* d_sum, const int64_t* d_dot,
+                            uint32_t scale_q32, uint32_t n, uint64_t* d_exp, int32_t* d_weight, int32_t* d_score) {
     if (n == 0) return 0;
-    if (!d_diff || !d_e || !d_sum || !d_exp || !d_weight) return IRIS_E_INVALID;
-    hipLaunchKernelGGL(softmax_terms_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, d_diff, d_e, d_sum, n,
-                       d_exp, d_weight);
+    if (!d_diff || !d_e || !d_sum || !d_dot || !d_exp || !d_weight || !d_score) return IRIS_E_INVALID;
+    hipLaunchKernelGGL(attention_numerics_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, d_diff, d_e, d_sum,
+                       d_dot, scale_q32, n, d_exp, d_weight, d_score);
     hipError_t st = hipGetLastError();
     if (st == hipSuccess) st = hipDeviceSynchronize();
     return (int)st;

@@ -242,63 +242,84 @@ __device__ inline int64_t softmax_exp_term(int64_t delta) {
     return 0;
 }
 
-// rte(x / c) for x >= 0: ops.rs:691-720 with a non-negative dividend.
-__device__ __forceinline__ uint64_t rte_div_small(uint64_t x, uint32_t c) {
-    uint64_t q = x / c;
-    const uint64_t twice = 2 * (x - q * c);
+// rte(x / c) (ops.rs:691-720) for a non-negative dividend below 2^32.
+__device__ __forceinline__ uint32_t rte_div_u32(uint32_t x, uint32_t c) {
+    uint32_t q = x / c;
+    const uint32_t twice = 2 * (x - q * c);
     if (twice > c || (twice == c && (q & 1))) q++;
     return q;
 }
 
-// acc_mul (ops.rs:685-689) of 0 <= a, b < 2^32: the product fits 64 bits.
-__device__ __forceinline__ uint64_t acc_mul_small(uint64_t a, uint64_t b) {
-    const uint64_t p = a * b;
-    uint64_t fl = p >> 32;
-    const uint64_t rem = p & 0xffffffffull;
-    if (rem > 0x80000000ull || (rem == 0x80000000ull && (fl & 1))) fl++;
+// acc_mul (ops.rs:685-689) of 0 <= a, b < 2^32: the product fits 64 bits,
+// and the rounded result stays below 2^32 when a or b is below 2^32 - 1.
+__device__ __forceinline__ uint32_t acc_mul_u32(uint32_t a, uint32_t b) {
+    const uint64_t p = (uint64_t)a * b;
+    uint32_t fl = (uint32_t)(p >> 32);
+    const uint32_t rem = (uint32_t)p;
+    if (rem > 0x80000000u || (rem == 0x80000000u && (fl & 1))) fl++;
     return fl;
 }
 
 // softmax_exp_term (ops.rs:508-556) of delta = -(diff << 16), diff >= 0:
 // the only deltas the softmax forms (a logit minus the row's maximum).
-// diff >= 2^20 is at or below the -16 cut: zero. Below it r < ln 2 < 1 in
-// Q32.32, so every acc_mul multiplies two values under 2^32, none of the
-// saturating sums can saturate, and the divisions by 2, 6, 24 and 120 are of
-// non-negative values: the general routine's integers with 64-bit operations.
+// diff >= 2^20 is at or below the -16 cut: zero; diff = 0 gives exactly one.
+// Otherwise 0 < r < ln 2 < 1 in Q32.32: every power and quotient of the
+// Taylor terms is below 2^32, none of the saturating sums can saturate, the
+// result of the nested sums lies in (0, 2^32), and the shift is at most 23,
+// so the general routine's integers come out of 32-bit operations. The
+// quotient by ln 2 starts from a float estimate (off by at most one, as
+// diff < 2^20 is exact in a float) and is corrected on the remainder.
 __device__ __forceinline__ uint64_t softmax_exp_diff(uint32_t diff) {
     if (diff >= (1u << 20)) return 0;
-    const uint64_t LN_2_BITS = 2977044472ull;
-    const uint64_t positive = (uint64_t)diff << 16;
-    const uint64_t shift = positive / LN_2_BITS;
-    const uint64_t r = positive - shift * LN_2_BITS;
-    const uint64_t r2 = acc_mul_small(r, r), r3 = acc_mul_small(r2, r);
-    const uint64_t r4 = acc_mul_small(r3, r), r5 = acc_mul_small(r4, r);
-    const int64_t approx = (int64_t)ONE_ACC - (int64_t)r + (int64_t)rte_div_small(r2, 2) -
-                           (int64_t)rte_div_small(r3, 6) + (int64_t)rte_div_small(r4, 24) -
-                           (int64_t)rte_div_small(r5, 120);
-    if (approx <= 0) return 0;
-    return (uint64_t)rshift_rte(approx, (uint32_t)shift);
+    if (diff == 0) return (uint64_t)ONE_ACC;
+    const int64_t LN_2_BITS = 2977044472LL;
+    const int64_t positive = (int64_t)diff << 16;
+    uint32_t shift = (uint32_t)((float)diff * (65536.0f / 2977044472.0f));
+    int64_t rl = positive - (int64_t)shift * LN_2_BITS;
+    if (rl < 0) {
+        shift--;
+        rl += LN_2_BITS;
+    } else if (rl >= LN_2_BITS) {
+        shift++;
+        rl -= LN_2_BITS;
+    }
+    const uint32_t r = (uint32_t)rl;
+    const uint32_t r2 = acc_mul_u32(r, r), r3 = acc_mul_u32(r2, r);
+    const uint32_t r4 = acc_mul_u32(r3, r), r5 = acc_mul_u32(r4, r);
+    // 1 - r + r2/2 - r3/6 + r4/24 - r5/120, modulo 2^32 (the true value is
+    // in (0, 2^32)).
+    const uint32_t approx = 0u - r + rte_div_u32(r2, 2) - rte_div_u32(r3, 6) + rte_div_u32(r4, 24) -
+                            rte_div_u32(r5, 120);
+    if (shift == 0) return approx;
+    uint32_t fl = approx >> shift;
+    const uint32_t rem = approx & ((1u << shift) - 1), half = 1u << (shift - 1);
+    if (rem > half || (rem == half && (fl & 1))) fl++;
+    return fl;
 }
 
 // attention_softmax_raw_weight (ops.rs:269-271), requantize(div_acc(e, sum)),
-// for 0 <= e <= 2^32 <= sum < 2^62 and inv_sum = 1.0 / sum: the quotient
-// (e << 32) / sum from a double estimate (off by at most one), made exact by
-// the integer remainder (exact modulo 2^64, and |remainder| < 2 * sum), then
-// rounded half to even as div_acc does, then requantized.
-__device__ __forceinline__ int32_t softmax_weight(uint64_t e, uint64_t sum, double inv_sum) {
-    uint64_t q = (uint64_t)((double)e * 4294967296.0 * inv_sum);
+// for 0 <= e <= 2^32 <= sum < 2^62 and q_scale = 2^32 / sum in double: the
+// quotient (e << 32) / sum from the double estimate e * q_scale (within
+// 2^-20 of the true quotient, so its floor is off by at most one), made
+// exact on the integer remainder (exact modulo 2^64, |remainder| < 2 * sum),
+// rounded half to even as div_acc does, then requantized (the quotient is at
+// most 2^32, the weight at most 2^16).
+__device__ __forceinline__ int32_t softmax_weight(uint64_t e, uint64_t sum, double q_scale) {
+    uint64_t q = (uint64_t)((double)e * q_scale);
     int64_t rem = (int64_t)((e << 32) - q * sum);
-    while (rem < 0) {
+    if (rem < 0) {
         q--;
         rem += (int64_t)sum;
-    }
-    while ((uint64_t)rem >= sum) {
+    } else if ((uint64_t)rem >= sum) {
         q++;
         rem -= (int64_t)sum;
     }
-    const uint64_t other = sum - (uint64_t)rem;
-    if ((uint64_t)rem > other || ((uint64_t)rem == other && (q & 1))) q++;
-    return requantize((int64_t)q);
+    const uint64_t twice = (uint64_t)rem << 1;
+    if (twice > sum || (twice == sum && (q & 1))) q++;
+    uint64_t w = q >> 16;
+    const uint32_t lo = (uint32_t)q & 0xffff;
+    if (lo > 0x8000 || (lo == 0x8000 && (w & 1))) w++;
+    return (int32_t)w;
 }
 
 // ops.rs:357-377
@@ -437,11 +458,12 @@ __device__ __forceinline__ void rotate_pair_q30(int32_t& a, int32_t& b, int64_t 
 
 // mistral.rs:130-145 after the wrapping sum.
 __device__ __forceinline__ int32_t scaled_score_from_sum(int64_t sum, uint32_t scale_q32) {
-    i128 scaled = ((i128)sum * (i128)scale_q32) >> 32;
-    i128 fl = scaled >> 16;
-    int64_t rem = (int64_t)(scaled - (fl << 16));
-    i128 r = (rem > 32768 || (rem == 32768 && (fl & 1))) ? fl + 1 : fl;
-    return clamp_i128_to_i32(r);
+    // floor(sum * scale / 2^32) = hi * scale + floor(lo * scale / 2^32) for
+    // sum = hi * 2^32 + lo (hi signed, lo unsigned); |.| < 2^63.
+    const int64_t hi = sum >> 32;
+    const uint64_t lo = (uint32_t)sum;
+    const int64_t scaled = hi * (int64_t)scale_q32 + (int64_t)((lo * scale_q32) >> 32);
+    return clamp_i64_to_i32(rshift_rte(scaled, 16));
 }
 
 // q8.rs:94-104: value / 2^shift, ties to even, saturated to i32.

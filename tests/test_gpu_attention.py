@@ -25,16 +25,16 @@ def device():
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
 
 
-def _softmax_terms(diff, e, s):
+def _numerics(diff, e, s, dot, scale):
     n = diff.size
     L = native.lib()
-    dd, de, ds = (native.DeviceBuffer.from_array(np.ascontiguousarray(a)) for a in (diff, e, s))
-    dexp, dw = native.DeviceBuffer(8 * n), native.DeviceBuffer(4 * n)
-    native.check(L.iris_softmax_terms(dd.ptr, de.ptr, ds.ptr, n, dexp.ptr, dw.ptr), "softmax terms")
-    return dexp.to_array(np.uint64, (n,)), dw.to_array(np.int32, (n,))
+    bufs = [native.DeviceBuffer.from_array(np.ascontiguousarray(a)) for a in (diff, e, s, dot)]
+    dexp, dw, dsc = native.DeviceBuffer(8 * n), native.DeviceBuffer(4 * n), native.DeviceBuffer(4 * n)
+    native.check(L.iris_attention_numerics(*[b.ptr for b in bufs], scale, n, dexp.ptr, dw.ptr, dsc.ptr), "numerics")
+    return dexp.to_array(np.uint64, (n,)), dw.to_array(np.int32, (n,)), dsc.to_array(np.int32, (n,))
 
 
-def test_softmax_terms_against_oracle():
+def test_attention_numerics_against_oracle():
     O = cpu.lib()
     # Every logit difference below the -16 cut, and a few at and past it.
     diff = np.arange(0, (1 << 20) + 8, dtype=np.uint32)
@@ -52,11 +52,21 @@ def test_softmax_terms_against_oracle():
                               np.uint64(1 << 32))
     es[:3] = [0, 1 << 32, 1 << 32]
     sums[:3] = [1 << 32, 1 << 32, (1 << 33) + 2]
-    got_e, got_w = _softmax_terms(diff, es, sums)
+    # Scores: wrapping sums q0*k0 + q1*k1 of full-range i32 pairs, through
+    # the oracle's two-element scaled_score (head size 128's scale).
+    qk = rng.integers(-2 ** 31, 2 ** 31, (n, 4), dtype=np.int64)
+    dots = ((qk[:, 0] * qk[:, 1]).astype(np.uint64) + (qk[:, 2] * qk[:, 3]).astype(np.uint64)).view(np.int64)
+    scale = O.dn_attention_scale_q32(128)
+    got_e, got_w, got_s = _numerics(diff, es, sums, dots, scale)
     want_e = np.array([O.dn_softmax_exp_term(-(int(d) << 16)) for d in diff], np.int64).astype(np.uint64)
     assert np.array_equal(got_e, want_e)
     want_w = np.array([O.dn_requantize(O.dn_div_acc(int(e), int(s))) for e, s in zip(es, sums)], np.int32)
     assert np.array_equal(got_w, want_w)
+    idx = np.arange(0, n, 7)
+    q2 = np.ascontiguousarray(qk[:, [0, 2]].astype(np.int32))
+    k2 = np.ascontiguousarray(qk[:, [1, 3]].astype(np.int32))
+    want_s = np.array([O.dn_scaled_score(q2[i], k2[i], 2, scale) for i in idx], np.int32)
+    assert np.array_equal(got_s[idx], want_s)
 
 
 def _check_pass(m, rows, max_positions=None):
