@@ -11,16 +11,17 @@
 // |sum| <= 4 * 128 * 2^14 < 2^31 for scores, 2 * 4096 * 2^14 for values).
 //
 // The softmax needs each row's first maximum before any exp term and the
-// full sum before any weight, so each workgroup walks its keys three times,
-// recomputing the scores (cheap on the matrix cores) instead of storing them:
-// (1) the first maximum, (2) the sum of exp terms, (3) the weights and the
-// weighted values. The weights never leave registers: the score tile's lane
-// layout is, up to a fixed permutation of the keys inside each 64-key step,
-// the A operand of the value product, and the value planes are written in
-// that permuted key order. A weight w < 2^16 is two digits unless
-// w >= 32640; those (at most two per row: the weights sum to 2^16 plus
-// rounding) are carried as w - 65536 plus 65536 * v added at the end, with
-// the residual of the first maximum (ops.rs:258-260).
+// full sum before any weight, so each workgroup walks its keys three times:
+// (1) scores and the first maximum; (2) scores again (cheap on the matrix
+// cores), the exp terms and their sum, the terms kept in an HBM store;
+// (3) the weights from the stored terms and the weighted values. The
+// weights never leave registers: the score tile's lane layout is, up to a
+// fixed permutation of the keys inside each 64-key step, the A operand of
+// the value product, and the value planes are written in that permuted key
+// order. A weight w <= 2^16 is two digits unless w >= 32640; those (at most
+// two per row: the weights sum to 2^16 plus rounding) are carried as
+// w - 65536 plus 65536 * v added at the end, with the residual of the first
+// maximum (ops.rs:258-260).
 //
 // Workgroup: one 16-row query tile of four query heads that share a KV head,
 // one wave per head. A tile whose queries or keys need five digits (|v|
@@ -269,20 +270,29 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
         }
     }
 
-    // (2) the sum of exp terms (non-negative, so no order and no saturation).
+    // (2) the sum of exp terms (non-negative, so no order and no saturation);
+    // each lane keeps its terms for (3) in the exp store, one 16-byte slot
+    // per tile (2^32, the maximum's term, as 0xffffffff: every other term is
+    // below 2^32 - 2^15).
     uint64_t sum = 0;
+    uint32_t* estore = p.e_store + ((size_t)head * p.qt_cap + qt) * p.ks_cap * 4 * 256 + lane * 4;
     load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
 #pragma unroll 1
     for (uint32_t kt = kt0; kt < kt1; kt++) {
         if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
         int32_t sc[4];
         tile_scores<HD, LQK>(a, kf, qf, sc);
+        uint32_t ev[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t key = kt * 16 + 4 * grp + i;
             const int64_t diff = (int64_t)best - sc[i];
-            if (visible(key)) sum += dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
+            uint64_t e = 0;
+            if (visible(key)) e = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
+            sum += e;
+            ev[i] = e > 0xffffffffull ? 0xffffffffu : (uint32_t)e;
         }
+        *(uint4*)(estore + (size_t)kt * 256) = make_uint4(ev[0], ev[1], ev[2], ev[3]);
 #pragma unroll
         for (int l = 0; l < LQK; l++)
 #pragma unroll
@@ -291,8 +301,10 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
     const double q_scale = qvalid ? 4294967296.0 / (double)sum : 0.0;
+    const double w_scale = qvalid ? 65536.0 / (double)sum : 0.0;
 
-    // (3) weights, their sum, and the weighted values.
+    // (3) weights from the stored terms (zero for keys out of view), their
+    // sum, and the weighted values.
     v4i pacc[DT][AP_V_PLANES + 1];
 #pragma unroll
     for (uint32_t dt = 0; dt < DT; dt++)
@@ -302,10 +314,10 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
     const int8_t* vbase = p.v + (size_t)g * p.ks_cap * DT * FRAG + lane * 16;
     int32_t wsum = 0;
     int32_t big[2] = {-1, -1};
-    load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+    uint4 en = *(const uint4*)(estore + (size_t)kt0 * 256);
 #pragma unroll 1
     for (uint32_t ks = ks0; ks < ks1; ks++) {
-        // The step's value operands, needed after its four score tiles.
+        // The step's value operands, needed after its four weight tiles.
         v4i vf[DT][AP_V_PLANES];
         const int8_t* vb = vbase + (size_t)ks * DT * FRAG;
 #pragma unroll
@@ -315,27 +327,23 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
         // The two weight digits of this lane's 16 keys: byte 4t + i of wf0/wf1
         // (tile t is shifted in as the last component).
         v4i wf0 = v4i{0, 0, 0, 0}, wf1 = v4i{0, 0, 0, 0};
-#pragma unroll 1
+#pragma unroll
         for (uint32_t t = 0; t < 4; t++) {
             const uint32_t kt = ks * 4 + t;
-            if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
-            int32_t sc[4];
-            tile_scores<HD, LQK>(a, kf, qf, sc);
+            const uint4 ec = en;
+            if (kt + 1 < kt1) en = *(const uint4*)(estore + (size_t)(kt + 1) * 256);
+            const uint32_t ev[4] = {ec.x, ec.y, ec.z, ec.w};
             uint32_t b0 = 0, b1 = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint32_t key = kt * 16 + 4 * grp + i;
-                int32_t w = 0;
-                if (visible(key)) {
-                    const int64_t diff = (int64_t)best - sc[i];
-                    const uint64_t e = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
-                    w = dn::softmax_weight(e, sum, q_scale);
-                    wsum += w;
-                    if (w >= BIG_WEIGHT) {
-                        if (big[0] < 0) big[0] = (int32_t)key;
-                        else big[1] = (int32_t)key;
-                        w -= 65536;
-                    }
+                const uint64_t e = ev[i] == 0xffffffffu ? (uint64_t)dn::ONE_ACC : ev[i];
+                int32_t w = dn::softmax_weight_fast(e, sum, w_scale, q_scale);
+                wsum += w;
+                if (w >= BIG_WEIGHT) {
+                    const int32_t key = (int32_t)(kt * 16 + 4 * grp + i);
+                    if (big[0] < 0) big[0] = key;
+                    else big[1] = key;
+                    w -= 65536;
                 }
                 const uint32_t u = (uint32_t)(w + 0x8080);  // two digits, each biased by 0x80
                 b0 |= ((u & 0xff) ^ 0x80) << (8 * i);
@@ -343,10 +351,6 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
             }
             wf0 = v4i{wf0[1], wf0[2], wf0[3], (int)b0};
             wf1 = v4i{wf1[1], wf1[2], wf1[3], (int)b1};
-#pragma unroll
-            for (int l = 0; l < LQK; l++)
-#pragma unroll
-                for (uint32_t ds = 0; ds < DS; ds++) kf[l][ds] = kn[l][ds];
         }
 #pragma unroll
         for (uint32_t dt = 0; dt < DT; dt++)
@@ -449,7 +453,7 @@ __global__ void attention_numerics_kernel(const uint32_t* diff, const uint64_t* 
     const uint32_t i = blockIdx.x * 256 + threadIdx.x;
     if (i >= n) return;
     e_out[i] = dn::softmax_exp_diff(diff[i]);
-    w_out[i] = dn::softmax_weight(e[i], sum[i], 4294967296.0 / (double)sum[i]);
+    w_out[i] = dn::softmax_weight_fast(e[i], sum[i], 65536.0 / (double)sum[i], 4294967296.0 / (double)sum[i]);
     score_out[i] = dn::scaled_score_from_sum(dot[i], scale_q32);
 }
 
@@ -468,7 +472,8 @@ int iris_attention_numerics(const uint32_t* d_diff, const uint64_t* d_e, const u
 
 bool iris_attention_prefill_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys) {
     const AttnPlanes& p = a.planes;
-    return tokens >= 2 && p.q && p.k && p.v && p.q_limbs && p.kv_limbs && (a.head_dim == 64 || a.head_dim == 128) &&
+    return tokens >= 2 && p.q && p.k && p.v && p.q_limbs && p.kv_limbs && p.e_store &&
+           (a.head_dim == 64 || a.head_dim == 128) &&
            a.heads % a.kv_heads == 0 && (a.heads / a.kv_heads) % 4 == 0 && (tokens + 15) / 16 <= p.qt_cap &&
            max_keys <= p.ks_cap * 64 && max_keys <= ATTN_MAX_KEYS;
 }

@@ -322,6 +322,19 @@ __device__ __forceinline__ int32_t softmax_weight(uint64_t e, uint64_t sum, doub
     return (int32_t)w;
 }
 
+// softmax_weight from a double estimate: y = e * 2^16 / sum (w_scale =
+// 2^16 / sum) is within 2^-30 of the real quotient, the Q32.32 rounding
+// moves it by at most 2^-17, so unless y lies within 2^-15 of a half
+// integer both roundings together give the integer nearest y; those rare
+// cases take the exact routine.
+__device__ __forceinline__ int32_t softmax_weight_fast(uint64_t e, uint64_t sum, double w_scale, double q_scale) {
+    const double t = (double)e * w_scale + 0.5;
+    const double fl = floor(t);
+    const double f = t - fl;
+    if (f < 0x1p-15 || f > 1.0 - 0x1p-15) return softmax_weight(e, sum, q_scale);
+    return (int32_t)fl;
+}
+
 // ops.rs:357-377
 __device__ inline int32_t tanh_act(int32_t x) {
     const int32_t LIN = 27 << 16, QUAD = 9 << 16, SAT = 3 << 16;

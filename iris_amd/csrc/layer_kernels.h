@@ -15,6 +15,7 @@ struct AttnPlanes {
     int8_t* v;               // [4][kv_heads][ks_cap][head_dim/16][1 KB]
     uint8_t* q_limbs;        // [heads][qt_cap]
     uint8_t* kv_limbs;       // [kv_heads][ks_cap][2]: keys', values' digits per 64-key step
+    uint32_t* e_store;       // [heads][qt_cap][ks_cap*4][64][4]: exp terms between the softmax passes
     uint32_t qt_cap;         // 16-row query tiles
     uint32_t ks_cap;         // 64-key steps
 };
@@ -26,6 +27,9 @@ inline uint64_t attn_q_planes_bytes(uint32_t heads, uint32_t head_dim, uint32_t 
 }
 inline uint64_t attn_kv_planes_bytes(uint32_t kv_heads, uint32_t head_dim, uint32_t ks_cap) {
     return 4ull * kv_heads * ks_cap * 64 * head_dim;
+}
+inline uint64_t attn_e_store_bytes(uint32_t heads, uint32_t qt_cap, uint32_t ks_cap) {
+    return 4096ull * heads * qt_cap * ks_cap;
 }
 
 struct AttnArgs {
@@ -50,7 +54,8 @@ struct AttnArgs {
     int32_t* chunk_wsum;     // [heads][ATTN_MAX_CHUNKS]
     int32_t* max_weight;     // [heads]: the first maximum's weight before the residual
     // Digit planes for the multi-row MFMA path (planes.q null: the scalar
-    // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes.
+    // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes /
+    // attn_e_store_bytes.
     AttnPlanes planes;
 };
 

@@ -774,6 +774,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
         alloc8((void**)&ap.v, attn_kv_planes_bytes(d.kv_heads, m->max_head_dim, ap.ks_cap));
         alloc8((void**)&ap.q_limbs, (uint64_t)d.heads * ap.qt_cap);
         alloc8((void**)&ap.kv_limbs, 2ull * d.kv_heads * ap.ks_cap);
+        alloc8((void**)&ap.e_store, attn_e_store_bytes(d.heads, ap.qt_cap, ap.ks_cap));
     }
     if (d.family == IRIS_FAMILY_GEMMA_DENSE) {
         const size_t lp = (size_t)d.layers * d.ple_width;
@@ -825,6 +826,7 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->attn_planes.v);
     hipFree(s->attn_planes.q_limbs);
     hipFree(s->attn_planes.kv_limbs);
+    hipFree(s->attn_planes.e_store);
     if (s->stream) hipStreamDestroy(s->stream);
     delete s;
 }
