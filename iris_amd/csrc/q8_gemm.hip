@@ -9,18 +9,21 @@
 // digits, x = sum_l 256^l d_l with d_l in [-128, 127] (the bytes of
 // x + 0x8080808080, each xor 0x80; five digits only for x >= 0x7F7F7F80),
 // and every digit plane is an int8 GEMM with exact int32 accumulation
-// (|sum| <= K * 2^14 < 2^31 for K < 2^17) on v_mfma_i32_16x16x64_i8.
+// (|sum| <= K * 2^14 < 2^31 for K < 2^17) on v_mfma_i32_32x32x32_i8.
 //
-// Operand layout. One 16x16x64 MFMA takes, in lane l, 16 bytes of row (or
-// token) l % 16 at k-offset 16 * (l / 16). Two consecutive 512-byte
-// tile-blocks of a 16-row weight tile ([half][16 rows][16 bytes] each) are
-// exactly that 1 KB A operand, so the weights need no second layout; the
-// digit planes are written in the same shape: plane l, 16-token tile tt and
-// 64-wide k-step ks form one 1 KB block at ((l * TT + tt) * KS + ks) * 1024.
-// Every operand the kernel stages is then one contiguous kilobyte, copied
-// from global memory straight into LDS (global_load_lds_dwordx4, no
-// registers in between) through a four-deep ring, and read back by each lane
-// as one conflict-free 16-byte LDS load.
+// Operand layout. One v_mfma_i32_32x32x32_i8 takes, in lane l, 16 bytes of
+// row (A) or column (B) l % 32 at reduction offset 16 * (l / 32), and
+// leaves output i of lane l at row 8 * (i / 4) + 4 * (l / 32) + i % 4,
+// column l % 32. (On gfx950 this instruction runs at about twice the rate
+// of the 16x16x64 one.) A weight operand, 32 rows by 32 k, is four 256-byte
+// runs of the Q8_0 tile layout (two 16-row tiles, two 16-byte halves of a
+// 32-wide block); the digit planes are written directly in operand shape:
+// plane l, 32-token tile tt and 32-wide k block kb form one 1 KB block at
+// ((l * TT + tt) * KB + kb) * 1024. Every operand is copied from global
+// memory straight into LDS (global_load_lds_dwordx4: each lane fetches its
+// own 16 bytes, the wave writes one contiguous kilobyte, no registers in
+// between) through a four-deep ring of 64-wide k steps, and read back by
+// each lane as one conflict-free 16-byte LDS load.
 #include "detnum_dev.h"
 #include "q8_epilogue.h"
 #include "q8_internal.h"
@@ -28,15 +31,25 @@
 namespace {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
 
 constexpr int PL_MAX = 5;                   // digit planes of an i32
-constexpr uint32_t GM_RT = 8;               // 16-row weight tiles per workgroup (128 rows)
-constexpr uint32_t GM_TT = 8;               // 16-token tiles per workgroup (128 tokens)
-constexpr uint32_t GM_THREADS = 256;        // 4 waves: 2 (row halves) x 2 (token halves)
-constexpr uint32_t GM_STAGES = 4;           // ring depth: three k-steps in flight
-constexpr uint32_t FRAG = 1024;             // bytes of one 16 x 64 operand
-constexpr uint32_t GM_STAGE = 32 * FRAG;    // 8 weight + up to 24 digit-plane operands
+constexpr uint32_t GM_TT = 4;               // 32-token tiles per workgroup (128 tokens)
+constexpr uint32_t FRAG = 1024;             // bytes of one 32 x 32 operand
 constexpr uint32_t GM_BAND = 8;             // row groups per band of the launch order
+
+// The two workgroup shapes: W waves in a (W/2) x 2 grid over 32 * W rows and
+// 128 tokens (W = 8: two waves per SIMD, 256 rows, for launches that fill
+// the chip; W = 4: one wave per SIMD, 128 rows, for smaller ones). A stage
+// is one 64-wide k step: 2W weight operands and up to 24 digit-plane ones.
+template <uint32_t W>
+struct GemmShape {
+    static constexpr uint32_t WAVES = W, THREADS = 64 * W, RT = W;  // RT: 32-row tiles
+    static constexpr uint32_t STAGE = (2 * W + 24) * FRAG;
+    static constexpr uint32_t STAGES = W == 8 ? 3 : 4;
+    static constexpr uint32_t OUT = 32 * W * 129 * 4;  // the output block, [row][128 tokens + 1]
+    static constexpr uint32_t SMEM = STAGES * STAGE > OUT ? STAGES * STAGE : OUT;
+};
 
 __device__ __forceinline__ uint64_t digits5(int32_t v) {
     return (uint64_t)((int64_t)v + 0x8080808080LL) ^ 0x8080808080ULL;
@@ -52,22 +65,22 @@ __device__ __forceinline__ uint32_t plane_byte4(uint64_t d0, uint64_t d1, uint64
            ((uint32_t)((d3 >> sh) & 0xff) << 24);
 }
 
-// The digit planes of one 16-token tile per workgroup, after the optional
+// The digit planes of one 32-token tile per workgroup, after the optional
 // rms_norm (ops.rs:98-114: mul_sat(mul_sat(v, scale), w)), in the operand
 // layout above, and the digits each token needs. Tokens past the end of the
 // last tile get zero digits.
 __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
-    __shared__ int32_t s_scale[16];
-    __shared__ int s_need[16];
+    __shared__ int32_t s_scale[32];
+    __shared__ int s_need[32];
     const uint32_t tt = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t K = a.w.cols, M = a.tokens, TT = (M + 15) / 16, KS = K / 64;
+    const uint32_t K = a.w.cols, M = a.tokens, TT = (M + 31) / 32, KB = K / 32;
     const bool norm = a.prologue == PRO_RMSNORM;
-    if (tid < 16) s_need[tid] = 1;
+    if (tid < 32) s_need[tid] = 1;
     if (norm) {
-        // Wave w sums the squares of tokens 4w..4w+3 of the tile (the sum of
+        // Wave w sums the squares of tokens 8w..8w+7 of the tile (the sum of
         // non-negative terms saturates the same way in any order).
-        for (uint32_t i = 0; i < 4; i++) {
-            const uint32_t t = tt * 16 + wave * 4 + i;
+        for (uint32_t i = 0; i < 8; i++) {
+            const uint32_t t = tt * 32 + wave * 8 + i;
             int64_t s = 0;
             if (t < M) {
                 const int32_t* x = a.x + (size_t)t * a.x_stride;
@@ -80,20 +93,20 @@ __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
                 }
             }
             for (int off = 32; off >= 1; off >>= 1) s = dn::acc_add_sat(s, __shfl_xor(s, off));
-            if (lane == 0) s_scale[wave * 4 + i] = t < M ? dn::rms_scale_from_sum(s, K, a.norm_eps) : 0;
+            if (lane == 0) s_scale[wave * 8 + i] = t < M ? dn::rms_scale_from_sum(s, K, a.norm_eps) : 0;
         }
     }
     __syncthreads();
-    // Lane l writes the 16 bytes of token l % 16 at k-offset 16 * (l / 16)
-    // of each k-step the wave takes.
-    const uint32_t tl = lane & 15, q = lane >> 4, t = tt * 16 + tl;
+    // Lane l writes the 16 bytes of token l % 32 at k-offset 16 * (l / 32)
+    // of each 32-wide block the wave takes.
+    const uint32_t tl = lane & 31, q = lane >> 5, t = tt * 32 + tl;
     const bool valid = t < M;
     const int32_t scale = norm ? s_scale[tl] : 0;
     const int32_t* x = a.x + (size_t)(valid ? t : 0) * a.x_stride;
-    const size_t lstride = (size_t)TT * KS * FRAG;
+    const size_t lstride = (size_t)TT * KB * FRAG;
     int need = 1;
-    for (uint32_t ks = wave; ks < KS; ks += 4) {
-        const uint32_t k0 = ks * 64 + q * 16;
+    for (uint32_t kb = wave; kb < KB; kb += 4) {
+        const uint32_t k0 = kb * 32 + q * 16;
         uint32_t out[PL_MAX][4];
 #pragma unroll
         for (int c = 0; c < 4; c++) {
@@ -111,16 +124,15 @@ __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
 #pragma unroll
             for (int l = 0; l < PL_MAX; l++) out[l][c] = plane_byte4(d0, d1, d2, d3, l);
         }
-        int8_t* dst = a.planes + ((size_t)tt * KS + ks) * FRAG + lane * 16;
+        int8_t* dst = a.planes + ((size_t)tt * KB + kb) * FRAG + lane * 16;
 #pragma unroll
         for (int l = 0; l < PL_MAX; l++)
             *(uint4*)(dst + l * lstride) = make_uint4(out[l][0], out[l][1], out[l][2], out[l][3]);
     }
-    need = max(need, __shfl_xor(need, 16));
     need = max(need, __shfl_xor(need, 32));
-    if (lane < 16) atomicMax(&s_need[lane], need);
+    if (lane < 32) atomicMax(&s_need[lane], need);
     __syncthreads();
-    if (tid < 16 && tt * 16 + tid < M) a.token_limbs[tt * 16 + tid] = s_need[tid];
+    if (tid < 32 && tt * 32 + tid < M) a.token_limbs[tt * 32 + tid] = s_need[tid];
 }
 
 template <int N>
@@ -133,43 +145,54 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// One pass of the workgroup over the whole k range: 8 weight tiles (rows
-// rt0*16 ..) times 2*TTW token tiles (from tt0) times LG digit planes. Wave
-// (wr, wt) accumulates weight tiles wr*4..wr*4+3 against token tiles
-// wt*TTW..: acc[i][j][l] is the int32 sum of plane l for its 16 x 16 block.
-// Operands past the last tile are clamped onto it (read, never stored).
-template <int LG, int TTW>
+// One pass of the workgroup over the whole k range: RT weight tiles of 32
+// rows (from 32-row tile rt0) times 2*TTW token tiles of 32 (from tt0) times
+// LG digit planes. Wave (wr, wt) accumulates weight tiles wr*2, wr*2+1
+// against token tiles wt*TTW..: acc[i][j][l] is the int32 sum of plane l
+// for its 32 x 32 block. A stage holds, for its two 32-wide k blocks s, the
+// weight operand of tile r at chunk 2r + s and the plane-l operand of token
+// tile j at 2RT + 2(l * 2TTW + j) + s (padded to a whole number of chunks
+// per wave with copies of chunk 0). Operands past the last tile are clamped
+// onto it (read, never stored).
+template <class G, int LG, int TTW>
 __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
-                                              v4i (&acc)[4][TTW][LG]) {
-    constexpr uint32_t TTWG = 2 * TTW;             // token tiles per pass
-    constexpr uint32_t CHUNKS = GM_RT + LG * TTWG; // 1 KB operands per stage
-    constexpr uint32_t PER_WAVE = CHUNKS / 4;
-    static_assert(CHUNKS % 4 == 0 && CHUNKS * FRAG <= GM_STAGE, "stage layout");
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wr = wave & 1, wt = wave >> 1;
+                                              v16i (&acc)[2][TTW][LG]) {
+    constexpr uint32_t TTWG = 2 * TTW;                      // token tiles per pass
+    constexpr uint32_t CHUNKS = 2 * G::RT + 2 * LG * TTWG;  // 1 KB operands per stage
+    constexpr uint32_t PER_WAVE = (CHUNKS + G::WAVES - 1) / G::WAVES;
+    constexpr uint32_t GM_RT = G::RT, GM_STAGES = G::STAGES, GM_STAGE = G::STAGE;
+    static_assert(PER_WAVE * G::WAVES * FRAG <= G::STAGE && PER_WAVE >= 2, "stage layout");
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wr = wave % (G::WAVES / 2), wt = wave / (G::WAVES / 2);
     const Q8View& w = a.w;
-    const uint32_t KS = w.cols / 64, TT = (a.tokens + 15) / 16;
-    const size_t lstride = (size_t)TT * KS * FRAG;
+    const uint32_t KS = w.cols / 64, KB = w.cols / 32, TT = (a.tokens + 31) / 32;
+    const size_t lstride = (size_t)TT * KB * FRAG;
 
-    // Operand c of a stage: c < 8 is weight tile rt0 + c, then plane l, token
-    // tile j at 8 + l * TTWG + j. Wave w copies operands w, w + 4, ...
+    // Wave w copies chunks w, w + W, ...: the first two are weight operands
+    // (advancing 1 KB of the tile layout per k step), the rest plane
+    // operands (advancing 2 KB).
     const int8_t* src[PER_WAVE];
+    uint32_t step[PER_WAVE];
 #pragma unroll
     for (uint32_t i = 0; i < PER_WAVE; i++) {
-        const uint32_t c = wave + 4 * i;
-        if (c < GM_RT) {
-            const uint32_t tile = min(rt0 + c, w.tiles - 1);
-            src[i] = (const int8_t*)w.qs + (size_t)tile * w.nb * Q8_TILE_BLOCK_BYTES + lane * 16;
+        const uint32_t c0 = wave + G::WAVES * i, c = c0 < CHUNKS ? c0 : 0;
+        step[i] = c < 2 * GM_RT ? FRAG : 2 * FRAG;
+        if (c < 2 * GM_RT) {
+            const uint32_t r = lane & 31, h = lane >> 5, sub = c & 1;
+            const uint32_t tile16 = min(2 * (rt0 + c / 2) + r / 16, w.tiles - 1);
+            src[i] = (const int8_t*)w.qs + ((size_t)tile16 * w.nb + sub) * Q8_TILE_BLOCK_BYTES + h * 256 + (r % 16) * 16;
         } else {
-            const uint32_t b = c - GM_RT, l = b / TTWG, tile = min(tt0 + b % TTWG, TT - 1);
-            src[i] = a.planes + l * lstride + (size_t)tile * KS * FRAG + lane * 16;
+            const uint32_t b = c - 2 * GM_RT, sub = b & 1, rest = b >> 1, l = rest / TTWG;
+            const uint32_t tile = min(tt0 + rest % TTWG, TT - 1);
+            src[i] = a.planes + l * lstride + ((size_t)tile * KB + sub) * FRAG + lane * 16;
         }
     }
     auto issue = [&](uint32_t ks) {
         int8_t* base = smem + (ks % GM_STAGES) * GM_STAGE;
 #pragma unroll
         for (uint32_t i = 0; i < PER_WAVE; i++)
-            __builtin_amdgcn_global_load_lds(src[i] + (size_t)ks * FRAG,
-                                             (__attribute__((address_space(3))) void*)(base + (wave + 4 * i) * FRAG),
+            __builtin_amdgcn_global_load_lds(src[i] + (size_t)ks * step[i],
+                                             (__attribute__((address_space(3))) void*)(base + (wave + G::WAVES * i) * FRAG),
                                              16, 0, 0);
     };
 
@@ -180,50 +203,54 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
         // This wave's copies for step ks are in LDS once at most the later
         // steps' copies are outstanding; the barrier makes every wave's
         // visible and frees the slot the next copy overwrites (read at ks-1).
-        if (ks + 2 < KS) wait_vmem<2 * PER_WAVE>();
+        if (GM_STAGES >= 4 && ks + 2 < KS) wait_vmem<(GM_STAGES >= 4 ? 2 : 1) * PER_WAVE>();
         else if (ks + 1 < KS) wait_vmem<PER_WAVE>();
         else wait_vmem<0>();
         lds_barrier();
         if (ks + GM_STAGES - 1 < KS) issue(ks + GM_STAGES - 1);
-        const int8_t* sA = smem + (ks % GM_STAGES) * GM_STAGE;
-        const int8_t* sB = sA + GM_RT * FRAG;
-        v4i fa[4];
+        const int8_t* st = smem + (ks % GM_STAGES) * GM_STAGE + lane * 16;
 #pragma unroll
-        for (int i = 0; i < 4; i++) fa[i] = *(const v4i*)(sA + (wr * 4 + i) * FRAG + lane * 16);
+        for (uint32_t sub = 0; sub < 2; sub++) {
+            v4i fa[2];
 #pragma unroll
-        for (int l = 0; l < LG; l++) {
-            v4i fb[TTW];
+            for (int i = 0; i < 2; i++) fa[i] = *(const v4i*)(st + (2 * (wr * 2 + i) + sub) * FRAG);
 #pragma unroll
-            for (int j = 0; j < TTW; j++) fb[j] = *(const v4i*)(sB + (l * TTWG + wt * TTW + j) * FRAG + lane * 16);
-#pragma unroll
-            for (int i = 0; i < 4; i++)
+            for (int l = 0; l < LG; l++) {
+                v4i fb[TTW];
 #pragma unroll
                 for (int j = 0; j < TTW; j++)
-                    acc[i][j][l] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j][l], 0, 0, 0);
+                    fb[j] = *(const v4i*)(st + (2 * GM_RT + 2 * (l * TTWG + wt * TTW + j) + sub) * FRAG);
+#pragma unroll
+                for (int i = 0; i < 2; i++)
+#pragma unroll
+                    for (int j = 0; j < TTW; j++)
+                        acc[i][j][l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i], fb[j], acc[i][j][l], 0, 0, 0);
+            }
         }
     }
     lds_barrier();  // every wave is done with the ring before it is reused
 }
 
-// Lane l holds rows 4 * (l / 16) + e of each weight tile for token l % 16 of
-// each token tile: recombine the planes, scale, round once, park the block
-// in LDS as [row][token], then run the epilogue row-fastest.
-template <int LG, int TTW>
+// Output e of lane l of a 32 x 32 block is row 8(e/4) + 4(l/32) + e%4,
+// token l % 32: recombine the planes, scale, round once, park the block in
+// LDS as [row][token], then run the epilogue row-fastest.
+template <class G, int LG, int TTW>
 __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
-                                              const v4i (&acc)[4][TTW][LG]) {
-    constexpr uint32_t NTOK = 32 * TTW, ROWS = GM_RT * 16, STRIDE = NTOK + 1;
-    static_assert(ROWS * STRIDE * 4 <= GM_STAGES * GM_STAGE, "output block must fit the ring");
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, wr = wave & 1, wt = wave >> 1;
+                                              const v16i (&acc)[2][TTW][LG]) {
+    constexpr uint32_t NTOK = 64 * TTW, ROWS = G::RT * 32, STRIDE = NTOK + 1;
+    static_assert(ROWS * STRIDE * 4 <= G::SMEM, "output block must fit the LDS");
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wr = wave % (G::WAVES / 2), wt = wave / (G::WAVES / 2);
     const Q8View& w = a.w;
     int32_t* sC = (int32_t*)smem;
 #pragma unroll
-    for (int i = 0; i < 4; i++) {
+    for (int i = 0; i < 2; i++) {
 #pragma unroll
         for (int j = 0; j < TTW; j++) {
-            const uint32_t tl = (wt * TTW + j) * 16 + (lane % 16);
+            const uint32_t tl = (wt * TTW + j) * 32 + (lane & 31);
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const uint32_t rl = (wr * 4 + i) * 16 + (lane / 16) * 4 + e, row = rt0 * 16 + rl;
+            for (int e = 0; e < 16; e++) {
+                const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4), row = rt0 * 32 + rl;
                 int64_t tot = 0;  // the row's integer dot product, |tot| < K * 2^38
 #pragma unroll
                 for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
@@ -233,62 +260,67 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
         }
     }
     __syncthreads();
-    for (uint32_t c = tid; c < ROWS * NTOK; c += GM_THREADS) {
+    for (uint32_t c = tid; c < ROWS * NTOK; c += G::THREADS) {
         const uint32_t rl = c % ROWS, tl = c / ROWS;
-        const uint32_t row = rt0 * 16 + rl, token = tt0 * 16 + tl;
+        const uint32_t row = rt0 * 32 + rl, token = tt0 * 32 + tl;
         if (row < w.rows && token < a.tokens)
             store_output(a, row, token, sC[rl * STRIDE + tl], sC[(rl ^ 1) * STRIDE + tl]);
     }
     __syncthreads();
 }
 
-template <int LG, int TTW>
+template <class G, int LG, int TTW>
 __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0) {
-    v4i acc[4][TTW][LG];
+    v16i acc[2][TTW][LG];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int j = 0; j < TTW; j++)
 #pragma unroll
-            for (int l = 0; l < LG; l++) acc[i][j][l] = v4i{0, 0, 0, 0};
-    gemm_mainloop<LG, TTW>(a, smem, rt0, tt0, acc);
-    gemm_epilogue<LG, TTW>(a, smem, rt0, tt0, acc);
+            for (int l = 0; l < LG; l++) acc[i][j][l] = v16i{};
+    gemm_mainloop<G, LG, TTW>(a, smem, rt0, tt0, acc);
+    gemm_epilogue<G, LG, TTW>(a, smem, rt0, tt0, acc);
 }
 
-// 128 weight rows x 128 tokens per workgroup, one wave per SIMD. Up to three
-// digit planes (the usual case) are accumulated side by side in one pass;
-// a block whose tokens need four or five takes two passes of 64 tokens.
-// Workgroups are ordered so that each XCD (blocks are dealt to the 8 XCDs
-// in turn) takes a contiguous range, walked in bands of 8 row groups with
-// the token groups inside a band, so blocks in flight together share
-// operands in their XCD's L2.
-__global__ __launch_bounds__(GM_THREADS, 1) void q8_gemm_row_kernel(const GemvArgs a) {
-    __shared__ __attribute__((aligned(1024))) int8_t smem[GM_STAGES * GM_STAGE];
-    __shared__ int s_limbs;
+// 32W weight rows x 128 tokens per workgroup. Up to three digit planes (the
+// usual case) are accumulated side by side in one pass; a block whose
+// tokens need four or five takes two passes of 64 tokens. Workgroups are
+// ordered so that each XCD (blocks are dealt to the 8 XCDs in turn) takes a
+// contiguous range, walked in bands of 8 row groups with the token groups
+// inside a band, so blocks in flight together share operands in their XCD's
+// L2.
+template <uint32_t W>
+__global__ __launch_bounds__(64 * W, 1) void q8_gemm_row_kernel(const GemvArgs a) {
+    using G = GemmShape<W>;
+    __shared__ __attribute__((aligned(1024))) int8_t smem[G::SMEM];
+    int& s_limbs = *(int*)smem;  // read before the ring is first filled
     const uint32_t tid = threadIdx.x;
-    const uint32_t TT = (a.tokens + 15) / 16;
-    const uint32_t n_rg = (a.w.tiles + GM_RT - 1) / GM_RT, n_tg = (TT + GM_TT - 1) / GM_TT, total = n_rg * n_tg;
+    const uint32_t TT = (a.tokens + 31) / 32;
+    const uint32_t n_rg = (a.w.tiles + 2 * G::RT - 1) / (2 * G::RT), n_tg = (TT + GM_TT - 1) / GM_TT;
+    const uint32_t total = n_rg * n_tg;
     uint32_t b = blockIdx.x;
     if (total % 8 == 0) b = (b % 8) * (total / 8) + b / 8;
     const uint32_t band = b / (GM_BAND * n_tg), first = band * GM_BAND, rows_in_band = min(GM_BAND, n_rg - first);
     const uint32_t r = b - band * GM_BAND * n_tg;
-    const uint32_t rt0 = (first + r % rows_in_band) * GM_RT, tt0 = (r / rows_in_band) * GM_TT;
+    const uint32_t rt0 = (first + r % rows_in_band) * G::RT, tt0 = (r / rows_in_band) * GM_TT;
 
     if (tid == 0) s_limbs = 1;
     __syncthreads();
-    if (tid < GM_TT * 16 && tt0 * 16 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 16 + tid]);
+    if (tid < GM_TT * 32 && tt0 * 32 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 32 + tid]);
     __syncthreads();
-    switch (s_limbs) {
-        case 1: gemm_pass<1, 4>(a, smem, rt0, tt0); break;
-        case 2: gemm_pass<2, 4>(a, smem, rt0, tt0); break;
-        case 3: gemm_pass<3, 4>(a, smem, rt0, tt0); break;
+    const int limbs = s_limbs;
+    __syncthreads();
+    switch (limbs) {
+        case 1: gemm_pass<G, 1, 2>(a, smem, rt0, tt0); break;
+        case 2: gemm_pass<G, 2, 2>(a, smem, rt0, tt0); break;
+        case 3: gemm_pass<G, 3, 2>(a, smem, rt0, tt0); break;
         case 4:
-            gemm_pass<4, 2>(a, smem, rt0, tt0);
-            gemm_pass<4, 2>(a, smem, rt0, tt0 + 4);
+            gemm_pass<G, 4, 1>(a, smem, rt0, tt0);
+            gemm_pass<G, 4, 1>(a, smem, rt0, tt0 + 2);
             break;
         default:
-            gemm_pass<5, 2>(a, smem, rt0, tt0);
-            gemm_pass<5, 2>(a, smem, rt0, tt0 + 4);
+            gemm_pass<G, 5, 1>(a, smem, rt0, tt0);
+            gemm_pass<G, 5, 1>(a, smem, rt0, tt0 + 2);
             break;
     }
 }
@@ -304,11 +336,17 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     if (!iris_gemm_applies(a) || a.x_stride % 4 || ((uintptr_t)a.x & 15) || ((uintptr_t)a.planes & 255))
         return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
-    const uint32_t TT = (a.tokens + 15) / 16;
+    const uint32_t TT = (a.tokens + 31) / 32;
     hipLaunchKernelGGL(digit_planes_kernel, dim3(TT), dim3(256), 0, stream, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return (int)st;
-    const uint32_t n_rg = (a.w.tiles + GM_RT - 1) / GM_RT, n_tg = (TT + GM_TT - 1) / GM_TT;
-    hipLaunchKernelGGL(q8_gemm_row_kernel, dim3(n_rg * n_tg), dim3(GM_THREADS), 0, stream, a);
+    // Two waves per SIMD and 256 rows when that still gives every CU a
+    // workgroup, else one wave per SIMD and 128 rows.
+    const uint32_t n_tg = (TT + GM_TT - 1) / GM_TT;
+    const uint32_t n8 = (a.w.tiles + 15) / 16 * n_tg, n4 = (a.w.tiles + 7) / 8 * n_tg;
+    if (n8 >= (uint32_t)iris_device_cus())
+        hipLaunchKernelGGL(q8_gemm_row_kernel<8>, dim3(n8), dim3(512), 0, stream, a);
+    else
+        hipLaunchKernelGGL(q8_gemm_row_kernel<4>, dim3(n4), dim3(256), 0, stream, a);
     return (int)hipGetLastError();
 }

@@ -689,6 +689,11 @@ int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) 
 
 void iris_gemv_prepare() { gemv_prepare_once(); }
 
+int iris_device_cus() {
+    gemv_prepare_once();
+    return g_num_cus;
+}
+
 int iris_select_launch(const GemvArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(select_embed_kernel, dim3(1), dim3(256), 0, stream, a);
     return (int)hipGetLastError();

@@ -112,9 +112,9 @@ struct GemvArgs {
 };
 
 // Bytes of the MFMA product's digit planes: 5 planes of the tokens rounded
-// up to whole 16-token tiles, times cols, 256-byte aligned.
+// up to whole 32-token tiles, times cols, 256-byte aligned.
 inline uint64_t gemm_planes_bytes(uint32_t cols, uint32_t tokens) {
-    return (5ull * ((tokens + 15ull) & ~15ull) * cols + 255) & ~255ull;
+    return (5ull * ((tokens + 31ull) & ~31ull) * cols + 255) & ~255ull;
 }
 
 // The MFMA GEMM for a multi-token product (row-scale matrix, planes set);
@@ -133,6 +133,8 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream);
 // Reads the device's CU count and raises the product kernels' LDS limit;
 // called before any launch can be captured into a graph.
 void iris_gemv_prepare();
+// Compute units of the current device (queried once).
+int iris_device_cus();
 
 // Packs raw Q8_0 rows (device memory, reference layout) into m's tiled layout
 // and fills its scales; `m` must have its buffers allocated for `mode`.

@@ -190,11 +190,14 @@ def grouped_activations(rng, tokens, cols):
     return x
 
 
-@pytest.mark.parametrize("tokens,rows,cols", [(603, 1024, 192), (603, 136, 4160), (300, 272, 64)])
+@pytest.mark.parametrize("tokens,rows,cols", [(603, 1024, 192), (603, 136, 4160), (300, 272, 64), (300, 22100, 128),
+                                              (200, 32768, 64)])
 def test_mfma_product_digit_paths(tokens, rows, cols):
     # Every digit count's code path (one to three planes side by side, four
-    # and five in two token halves), one-step, short and long k loops, and
-    # launches whose block count does and does not split evenly over the XCDs.
+    # and five in two token halves), one-step, short and long k loops,
+    # launches whose block count does and does not split evenly over the
+    # XCDs, and both workgroup shapes (256-row blocks when the launch fills
+    # every CU: the last two cases).
     rng = np.random.default_rng(tokens + rows + cols)
     raw = synth.q8_matrix(synth.tensor_seed(11, rows), rows, cols, synth.scale_base_for(cols), True)
     m = Q8Matrix.from_bytes(raw, rows, cols)
