@@ -15,10 +15,12 @@
 // the step counter live in device memory, so a decode pass is the same
 // launch sequence every time and is captured once as a HIP graph.
 #include <algorithm>
+#include <atomic>
 #include <cstdlib>
 #include <cstring>
 #include <map>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "layer_kernels.h"
@@ -389,7 +391,21 @@ void iris_model_free(IrisModel* m) {
 
 // ---------------------------------------------------------------- session
 
-static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
+// Where a checkpointing pass leaves each layer's rows: a device copy per
+// layer, and an event recorded on the pass's stream once it is made.
+struct CkptSink {
+    int32_t* dev;        // [layers][rows][hidden]
+    hipEvent_t* events;  // [layers]
+};
+
+static int checkpoint_layer(IrisSession* s, const CkptSink* sink, uint32_t l, uint32_t rows) {
+    if (!sink) return 0;
+    const size_t n = (size_t)rows * s->model->d.hidden;
+    RT_CHECK(hipMemcpyAsync(sink->dev + l * n, s->x, n * 4, hipMemcpyDeviceToDevice, s->stream));
+    return (int)hipEventRecord(sink->events[l], s->stream);
+}
+
+static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     const uint32_t H = d.hidden;
@@ -483,9 +499,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
         g.residual_stride = H;
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
-        if (layer_rows_out)
-            RT_CHECK(hipMemcpyAsync(layer_rows_out + (size_t)l * rows * H, s->x, (size_t)rows * H * 4,
-                                    hipMemcpyDeviceToHost, st));
+        RT_CHECK(checkpoint_layer(s, sink, l, rows));
     }
     return 0;
 }
@@ -493,7 +507,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) 
 // One gemma-dense pass (crates/inference/kernels/src/prefill_range.rs:307-958
 // per layer, the PLE prepare of view_kernels.rs:59-99 first): eleven launches
 // per layer.
-static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
+static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     const uint32_t H = d.hidden, P = d.ple_width, LP = d.layers * d.ple_width;
@@ -645,16 +659,14 @@ static int gemma_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
         RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
         RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ple, d.norm_eps, s->attended, H, L.layer_scalar,
                                            s->x, H, H, rows, st));
-        if (layer_rows_out)
-            RT_CHECK(hipMemcpyAsync(layer_rows_out + (size_t)l * rows * H, s->x, (size_t)rows * H * 4,
-                                    hipMemcpyDeviceToHost, st));
+        RT_CHECK(checkpoint_layer(s, sink, l, rows));
     }
     return 0;
 }
 
-static int session_pass(IrisSession* s, uint32_t rows, int32_t* layer_rows_out) {
-    if (s->model->d.family == IRIS_FAMILY_GEMMA_DENSE) return gemma_pass(s, rows, layer_rows_out);
-    return mistral_pass(s, rows, layer_rows_out);
+static int session_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+    if (s->model->d.family == IRIS_FAMILY_GEMMA_DENSE) return gemma_pass(s, rows, sink);
+    return mistral_pass(s, rows, sink);
 }
 
 static int session_head_select(IrisSession* s, uint32_t rows) {
@@ -827,6 +839,11 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->attn_planes.q_limbs);
     hipFree(s->attn_planes.kv_limbs);
     hipFree(s->attn_planes.e_store);
+    hipFree(s->ckpt_dev);
+    if (s->ckpt_host) hipHostFree(s->ckpt_host);
+    for (auto e : s->ckpt_events)
+        if (e) hipEventDestroy(e);
+    if (s->copy_stream) hipStreamDestroy(s->copy_stream);
     if (s->stream) hipStreamDestroy(s->stream);
     delete s;
 }
@@ -879,30 +896,69 @@ int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt
     return 0;
 }
 
+// Staging for the per-layer checkpoints of passes of up to max_rows rows:
+// device copies, pinned host copies, a copy stream and per-layer events.
+static int ensure_checkpoint_space(IrisSession* s) {
+    if (s->ckpt_dev) return 0;
+    const IrisModelDesc& d = s->model->d;
+    const size_t bytes = (size_t)d.layers * s->max_rows * d.hidden * 4;
+    RT_CHECK(hipMalloc((void**)&s->ckpt_dev, bytes));
+    RT_CHECK(hipHostMalloc((void**)&s->ckpt_host, bytes, hipHostMallocDefault));
+    RT_CHECK(hipStreamCreate(&s->copy_stream));
+    s->ckpt_events.assign(2 * (size_t)d.layers, nullptr);
+    for (auto& e : s->ckpt_events) RT_CHECK(hipEventCreateWithFlags(&e, hipEventDisableTiming));
+    return 0;
+}
+
+// The pass runs on the session's stream, copying each layer's rows aside on
+// the device as it finishes; a second stream brings them to pinned host
+// memory behind it, and host threads hash (and copy out) each layer as it
+// arrives, so the transfers and the hashing overlap the later layers.
 int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, int32_t* out_rows,
                             uint8_t* out_hashes) {
     if (!s || !ids || count == 0) return IRIS_E_INVALID;
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     if (count > s->max_rows || count > d.max_positions) return IRIS_E_RANGE;
-    std::vector<int32_t> rows;
-    int32_t* dst = out_rows;
-    if (!dst && out_hashes) {
-        try {
-            rows.resize((size_t)d.layers * count * d.hidden);
-        } catch (...) {
-            return IRIS_E_NOMEM;
-        }
-        dst = rows.data();
+    if (!out_rows && !out_hashes) {
+        RT_CHECK(session_reset_and_embed(s, ids, count));
+        RT_CHECK(session_pass(s, count, nullptr));
+        return (int)hipStreamSynchronize(s->stream);
     }
+    RT_CHECK(ensure_checkpoint_space(s));
+    const uint32_t layers = d.layers;
+    const size_t n = (size_t)count * d.hidden;
+    hipEvent_t* on_device = s->ckpt_events.data();
+    hipEvent_t* on_host = on_device + layers;
+    const CkptSink sink{s->ckpt_dev, on_device};
     RT_CHECK(session_reset_and_embed(s, ids, count));
-    RT_CHECK(session_pass(s, count, dst));
+    RT_CHECK(session_pass(s, count, &sink));
+    for (uint32_t l = 0; l < layers; l++) {
+        RT_CHECK(hipStreamWaitEvent(s->copy_stream, on_device[l], 0));
+        RT_CHECK(hipMemcpyAsync(s->ckpt_host + l * n * 4, s->ckpt_dev + l * n, n * 4, hipMemcpyDeviceToHost,
+                                s->copy_stream));
+        RT_CHECK(hipEventRecord(on_host[l], s->copy_stream));
+    }
+    const unsigned hw = std::thread::hardware_concurrency();
+    const uint32_t workers = std::max(1u, std::min({layers, 16u, hw ? hw : 1u}));
+    std::atomic<int> status{0};
+    std::vector<std::thread> pool;
+    for (uint32_t t = 0; t < workers; t++)
+        pool.emplace_back([&, t] {
+            for (uint32_t l = t; l < layers; l += workers) {
+                const hipError_t st = hipEventSynchronize(on_host[l]);
+                if (st != hipSuccess) {
+                    status = (int)st;
+                    continue;
+                }
+                const uint8_t* rows = s->ckpt_host + l * n * 4;
+                if (out_rows) std::memcpy(out_rows + l * n, rows, n * 4);
+                if (out_hashes) iris_sha256(rows, n * 4, out_hashes + 32 * l);
+            }
+        });
+    for (auto& th : pool) th.join();
     RT_CHECK(hipStreamSynchronize(s->stream));
-    if (out_hashes)
-        for (uint32_t l = 0; l < d.layers; l++)
-            iris_sha256((const uint8_t*)(dst + (size_t)l * count * d.hidden), (size_t)count * d.hidden * 4,
-                        out_hashes + 32 * l);
-    return 0;
+    return status;
 }
 
 int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, double* ms) {

@@ -87,6 +87,11 @@ struct IrisSession {
     int32_t* attn_max_weight = nullptr;
     // multi-row attention digit planes (null for single-row sessions)
     AttnPlanes attn_planes{};
+    // per-layer checkpoint staging, made on the first checkpointing pass
+    int32_t* ckpt_dev = nullptr;              // [layers][max_rows][hidden]
+    uint8_t* ckpt_host = nullptr;             // pinned, same shape
+    hipStream_t copy_stream = nullptr;
+    std::vector<hipEvent_t> ckpt_events;      // [2][layers]: rows copied on the device, on the host
     hipGraphExec_t graph_exec = nullptr;
     bool graph_keep_logits = false;
 };

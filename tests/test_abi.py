@@ -36,6 +36,9 @@ def test_layer_hash_is_sha256():
     # FIPS 180-4 vectors plus lengths around the padding boundary.
     import hashlib
     from iris_amd.direct import sha256
-    for data in [b"", b"abc", b"a" * 55, b"a" * 56, b"a" * 64, bytes(range(256)) * 9]:
+    import numpy as np
+    rng = np.random.default_rng(5)
+    longer = [rng.integers(0, 256, n, dtype=np.uint8).tobytes() for n in (1000, 65536 + 17, 3 << 20)]
+    for data in [b"", b"abc", b"a" * 55, b"a" * 56, b"a" * 64, bytes(range(256)) * 9] + longer:
         assert sha256(data) == hashlib.sha256(data).hexdigest()
     assert sha256(b"abc") == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
