@@ -15,6 +15,11 @@ The JSON line also carries:
   activations + outputs;
 - decode_roofline: the whole decode step against HBM (weights + KV cache
   read per token);
+- teacher_forced: the 2048-row teacher-forced chain pass on the same model
+  (device time of the pass; wall time with the per-layer SHA-256
+  checkpoints) and its gate|up product (M=2048, K=4096, N=28672) on the
+  int8 matrix cores, against the 5.0 POP/s dense int8 peak (the executed
+  MFMA work counts each signed byte digit plane of the activations);
 - cpu_baseline: the CPU oracle (a C restatement of the reference's kernels)
   timed on a bounded sample of the same decode on this host's cores.
 """
@@ -41,6 +46,7 @@ PEAK_HBM_GBPS = 8000.0
 GEMV_TRAFFIC_BYTES = 59_314_000
 PROMPT = 512  # the prompt length of the timed workload
 DECODE_TOKENS = 512
+TEACHER_FORCED_ROWS = 2048
 
 
 def log(msg):
@@ -118,6 +124,15 @@ def main():
     roof = gemv_roofline(decode_timing)
     log(f"GEMV {roof['avg_launch_us']} us = {roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of peak)")
 
+    # The teacher-forced chain pass (2048 rows, per-layer checkpoint hashes)
+    # on the same model, and its largest product on the int8 matrix cores.
+    bench.session.free()
+    tf = decode_timing.time_teacher_forced_session(bench.dm, bench.vocab, TEACHER_FORCED_ROWS)
+    log(f"teacher-forced {TEACHER_FORCED_ROWS} rows: pass {tf['pass_ms']} ms, with checkpoints {tf['checkpoint_ms']} ms")
+    bench.dm.free()
+    gemm = decode_timing.time_gemm(TEACHER_FORCED_ROWS)
+    log(f"MFMA GEMM {gemm['shape']}: {gemm['us']} us = {gemm['mfma_tops']} TOP/s ({100 * gemm['frac']:.1f}% of int8 peak)")
+
     base = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
@@ -137,6 +152,8 @@ def main():
                             "bytes_per_token": int(per_token)},
         "prompt_pass_ms": round(prefill_ms, 2),
         "deterministic_rerun": deterministic,
+        "teacher_forced": dict(tf, workload="mistral-7b-shape chain pass over 2048 uniform ids, "
+                                            "per-layer SHA-256 checkpoints", mfma_gemm=gemm),
         "cpu_baseline": base,
     }
     print(json.dumps(line), flush=True)

@@ -109,6 +109,12 @@ int iris_memcpy_d2d(void* dst, const void* src, uint64_t bytes);
 int iris_time_product(const Q8GpuMatrix* const* matrices, uint32_t count, const int32_t* d_activations,
                       uint32_t tokens, int32_t* d_out, uint32_t iterations, double* ms_per_product);
 
+/* As iris_time_product for one matrix through q8gpu_product_device_ws: with
+ * the work space, multi-token products of row-scale matrices run on the int8
+ * matrix cores (digit planes plus the MFMA GEMM), and this times them. */
+int iris_time_product_ws(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens, int32_t* d_out,
+                         void* d_workspace, uint64_t workspace_bytes, uint32_t iterations, double* ms_per_product);
+
 /* ------------------------------------------------------------------------
  * The deterministic token loop, device-resident.
  *

@@ -324,4 +324,28 @@ int iris_time_product(const Q8GpuMatrix* const* ms, uint32_t count, const int32_
     return rc;
 }
 
+int iris_time_product_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
+                         void* d_workspace, uint64_t workspace_bytes, uint32_t iterations, double* ms_per_product) {
+    if (!m || !ms_per_product || iterations == 0) return IRIS_E_INVALID;
+    hipStream_t s = nullptr;
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t st = hipStreamCreate(&s);
+    if (st == hipSuccess) st = hipEventCreate(&e0);
+    if (st == hipSuccess) st = hipEventCreate(&e1);
+    int rc = (int)st;
+    if (rc == 0) rc = q8gpu_product_device_ws(m, d_act, tokens, d_out, d_workspace, workspace_bytes, s);
+    if (rc == 0) rc = (int)hipEventRecord(e0, s);
+    for (uint32_t i = 0; rc == 0 && i < iterations; i++)
+        rc = q8gpu_product_device_ws(m, d_act, tokens, d_out, d_workspace, workspace_bytes, s);
+    if (rc == 0) rc = (int)hipEventRecord(e1, s);
+    if (rc == 0) rc = (int)hipEventSynchronize(e1);
+    float elapsed = 0.f;
+    if (rc == 0) rc = (int)hipEventElapsedTime(&elapsed, e0, e1);
+    if (rc == 0) *ms_per_product = (double)elapsed / iterations;
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    if (s) hipStreamDestroy(s);
+    return rc;
+}
+
 }  // extern "C"

@@ -72,6 +72,59 @@ def time_gemv(iterations: int = 200, n: int = GEMV_N, k: int = GEMV_K) -> dict:
             "algorithmic_bytes": gemv_algorithmic_bytes(n, k)}
 
 
+INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
+
+
+def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iterations: int = 20,
+              magnitude_bits: int = 21) -> dict:
+    """Average duration of one multi-token Q8_0 product on the int8 matrix
+    cores (digit planes + MFMA GEMM) at the gate|up shape of the 2048-row
+    pass, with activations of `magnitude_bits` bits (three signed byte
+    digits for the default, as the normalised inputs of that pass have).
+    The matrix-core work is 2 * tokens * n * k per digit plane."""
+    from .tensor import Q8Matrix
+
+    raw = synth.q8_matrix(synth.tensor_seed(3, 1), n, k, synth.scale_base_for(k), True)
+    m = Q8Matrix.from_bytes(raw, n, k)
+    rng = np.random.default_rng(4)
+    half = 1 << (magnitude_bits - 1)
+    x = rng.integers(-half, half, (tokens, k)).astype(np.int32)
+    dx = native.DeviceBuffer.from_array(x)
+    dout = native.DeviceBuffer(tokens * n * 4)
+    L = native.lib()
+    ws_bytes = L.q8gpu_workspace_bytes(m.handle, tokens)
+    ws = native.DeviceBuffer(ws_bytes)
+    ms = C.c_double()
+    native.check(L.iris_time_product_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, iterations,
+                                        C.byref(ms)), "time GEMM")
+    m.free()
+    digits = 3 if magnitude_bits <= 24 else 4
+    ops = 2.0 * tokens * n * k * digits
+    tops = ops / (ms.value * 1e-3) / 1e12
+    return {"shape": f"M={tokens} K={k} N={n}", "us": round(ms.value * 1e3, 1), "digit_planes": digits,
+            "mfma_tops": round(tops, 1), "peak_tops": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
+            "product_tops": round(tops / digits, 1)}
+
+
+def time_teacher_forced_session(dm, vocab: int, rows: int = 2048, repeats: int = 2) -> dict:
+    """The teacher-forced pass of every layer over `rows` uniform-random ids
+    on an uploaded model: device time of the pass (HIP events), and the wall
+    time of the per-layer checkpoint call (pass, rows to pinned host memory,
+    one SHA-256 per layer), after one untimed call that sets up its staging."""
+    import time
+    session = Session(dm, rows, rows)
+    ids = synth.token_ids(PROMPT_SEED, rows, vocab)
+    device_ms = min(session.time_pass(ids) for _ in range(repeats))
+    _, hashes = session.layer_pass(ids, keep_rows=False)
+    t = time.perf_counter()
+    _, hashes2 = session.layer_pass(ids, keep_rows=False)
+    wall_ms = (time.perf_counter() - t) * 1e3
+    session.free()
+    return {"rows": rows, "pass_ms": round(device_ms, 2), "checkpoint_ms": round(wall_ms, 2),
+            "rows_per_s": round(rows / (wall_ms * 1e-3), 1), "layers": len(hashes),
+            "repeatable": hashes2 == hashes, "last_layer_sha256": hashes[-1]}
+
+
 class DecodeBench:
     """Mistral-7B-shape model on the device with a session sized for a
     512-token prompt followed by `max_steps` decode steps."""
@@ -106,28 +159,16 @@ class DecodeBench:
 
 
 def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None) -> dict:
-    """One pass of every layer over `rows` uniform-random token ids at
-    Mistral-7B shape: the device time of the pass alone (HIP events), and
-    the wall time of the full per-layer checkpoint call (pass, rows copied
-    to the host, one SHA-256 per layer)."""
-    import time
+    """time_teacher_forced_session on a freshly uploaded Mistral-7B-shape model."""
     log = log or (lambda msg: None)
     model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
     dm = DeviceModel(model)
     vocab = model.vocab
     del model.tensors
     log("model on device")
-    session = Session(dm, rows, rows)
-    ids = synth.token_ids(PROMPT_SEED, rows, vocab)
-    device_ms = [session.time_pass(ids) for _ in range(repeats)]
-    log(f"device pass ms {device_ms}")
-    t = time.perf_counter()
-    _, hashes = session.layer_pass(ids, keep_rows=False)
-    wall_ms = (time.perf_counter() - t) * 1e3
-    session.free()
+    r = time_teacher_forced_session(dm, vocab, rows, repeats)
     dm.free()
-    return {"rows": rows, "device_ms": min(device_ms), "checkpoint_wall_ms": wall_ms,
-            "layers": len(hashes), "last_hash": hashes[-1]}
+    return r
 
 
 def main(argv=None):
@@ -139,8 +180,12 @@ def main(argv=None):
                     help="first run a 256 MiB device-to-device copy (byte-counter calibration)")
     ap.add_argument("--pass-rows", type=int, default=0,
                     help="time only the teacher-forced pass over this many rows")
+    ap.add_argument("--gemm-only", action="store_true", help="time only the MFMA product at the gate|up shape")
     args = ap.parse_args(argv)
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    if args.gemm_only:
+        print(json.dumps(time_gemm()), flush=True)
+        return
     if args.pass_rows:
         r = time_teacher_forced(args.pass_rows, log=lambda m: print(m, file=sys.stderr, flush=True))
         print(json.dumps(r), flush=True)
