@@ -22,7 +22,7 @@ int32_t* g_scratch_ws = nullptr;  // the MFMA product's digit planes
 size_t g_scratch_act_bytes = 0, g_scratch_out_bytes = 0, g_scratch_ws_bytes = 0;
 
 // Work space of a multi-token product: 5 digit planes of the activations
-// (256-byte aligned), then one digit count per token.
+// (256-byte aligned), then one digit count and one norm scale per token.
 uint64_t planes_bytes(uint32_t cols, uint32_t tokens) { return gemm_planes_bytes(cols, tokens); }
 
 hipError_t reserve(int32_t** buf, size_t* cap, size_t bytes) {
@@ -226,7 +226,7 @@ int q8gpu_product_device(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t to
 
 uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* m, uint32_t tokens) {
     if (!m || tokens < 2) return 0;
-    return planes_bytes(m->cols, tokens) + 4ull * tokens;
+    return planes_bytes(m->cols, tokens) + 8ull * tokens;
 }
 
 int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,

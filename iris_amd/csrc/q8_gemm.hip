@@ -65,47 +65,52 @@ __device__ __forceinline__ uint32_t plane_byte4(uint64_t d0, uint64_t d1, uint64
            ((uint32_t)((d3 >> sh) & 0xff) << 24);
 }
 
-// The digit planes of one 32-token tile per workgroup, after the optional
-// rms_norm (ops.rs:98-114: mul_sat(mul_sat(v, scale), w)), in the operand
-// layout above, and the digits each token needs. Tokens past the end of the
-// last tile get zero digits.
+// Per token, one wave each: the digit count reset to one and, under the
+// rms_norm prologue, the token's scale (ops.rs:98-114, rms_norm_scale of the
+// order-free saturating sum of squares) at token_limbs[tokens + t].
+__global__ __launch_bounds__(256) void token_prep_kernel(const GemvArgs a) {
+    const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= a.tokens) return;
+    if (a.prologue == PRO_RMSNORM) {
+        const uint32_t K = a.w.cols;
+        const int32_t* x = a.x + (size_t)t * a.x_stride;
+        int64_t s = 0;
+        for (uint32_t k = lane * 4; k < K; k += 256) {
+            const int4 v = *(const int4*)(x + k);
+            s = dn::acc_add_sat(s, (int64_t)v.x * v.x);
+            s = dn::acc_add_sat(s, (int64_t)v.y * v.y);
+            s = dn::acc_add_sat(s, (int64_t)v.z * v.z);
+            s = dn::acc_add_sat(s, (int64_t)v.w * v.w);
+        }
+        for (int off = 32; off >= 1; off >>= 1) s = dn::acc_add_sat(s, __shfl_xor(s, off));
+        if (lane == 0) a.token_limbs[a.tokens + t] = dn::rms_scale_from_sum(s, K, a.norm_eps);
+    }
+    if (lane == 0) a.token_limbs[t] = 1;
+}
+
+constexpr uint32_t PLANE_KB = 16;  // 32-wide k blocks per digit-plane workgroup
+
+// The digit planes of one 32-token tile over PLANE_KB k blocks per
+// workgroup, after the optional rms_norm (mul_sat(mul_sat(v, scale), w)),
+// in the operand layout above; each token's digit count is raised to what
+// these values need. Tokens past the end of the last tile get zero digits.
 __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
-    __shared__ int32_t s_scale[32];
     __shared__ int s_need[32];
     const uint32_t tt = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t K = a.w.cols, M = a.tokens, TT = (M + 31) / 32, KB = K / 32;
+    const uint32_t kb0 = blockIdx.y * PLANE_KB, kb1 = min(kb0 + PLANE_KB, KB);
     const bool norm = a.prologue == PRO_RMSNORM;
     if (tid < 32) s_need[tid] = 1;
-    if (norm) {
-        // Wave w sums the squares of tokens 8w..8w+7 of the tile (the sum of
-        // non-negative terms saturates the same way in any order).
-        for (uint32_t i = 0; i < 8; i++) {
-            const uint32_t t = tt * 32 + wave * 8 + i;
-            int64_t s = 0;
-            if (t < M) {
-                const int32_t* x = a.x + (size_t)t * a.x_stride;
-                for (uint32_t k = lane * 4; k < K; k += 256) {
-                    const int4 v = *(const int4*)(x + k);
-                    s = dn::acc_add_sat(s, (int64_t)v.x * v.x);
-                    s = dn::acc_add_sat(s, (int64_t)v.y * v.y);
-                    s = dn::acc_add_sat(s, (int64_t)v.z * v.z);
-                    s = dn::acc_add_sat(s, (int64_t)v.w * v.w);
-                }
-            }
-            for (int off = 32; off >= 1; off >>= 1) s = dn::acc_add_sat(s, __shfl_xor(s, off));
-            if (lane == 0) s_scale[wave * 8 + i] = t < M ? dn::rms_scale_from_sum(s, K, a.norm_eps) : 0;
-        }
-    }
     __syncthreads();
     // Lane l writes the 16 bytes of token l % 32 at k-offset 16 * (l / 32)
     // of each 32-wide block the wave takes.
     const uint32_t tl = lane & 31, q = lane >> 5, t = tt * 32 + tl;
     const bool valid = t < M;
-    const int32_t scale = norm ? s_scale[tl] : 0;
+    const int32_t scale = norm && valid ? a.token_limbs[M + t] : 0;
     const int32_t* x = a.x + (size_t)(valid ? t : 0) * a.x_stride;
     const size_t lstride = (size_t)TT * KB * FRAG;
     int need = 1;
-    for (uint32_t kb = wave; kb < KB; kb += 4) {
+    for (uint32_t kb = kb0 + wave; kb < kb1; kb += 4) {
         const uint32_t k0 = kb * 32 + q * 16;
         uint32_t out[PL_MAX][4];
 #pragma unroll
@@ -132,7 +137,7 @@ __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
     need = max(need, __shfl_xor(need, 32));
     if (lane < 32) atomicMax(&s_need[lane], need);
     __syncthreads();
-    if (tid < 32 && tt * 32 + tid < M) a.token_limbs[tt * 32 + tid] = s_need[tid];
+    if (tid < 32 && tt * 32 + tid < M && s_need[tid] > 1) atomicMax(&a.token_limbs[tt * 32 + tid], s_need[tid]);
 }
 
 template <int N>
@@ -336,8 +341,9 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     if (!iris_gemm_applies(a) || a.x_stride % 4 || ((uintptr_t)a.x & 15) || ((uintptr_t)a.planes & 255))
         return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
-    const uint32_t TT = (a.tokens + 31) / 32;
-    hipLaunchKernelGGL(digit_planes_kernel, dim3(TT), dim3(256), 0, stream, a);
+    const uint32_t TT = (a.tokens + 31) / 32, KB = a.w.cols / 32;
+    hipLaunchKernelGGL(token_prep_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(digit_planes_kernel, dim3(TT, (KB + PLANE_KB - 1) / PLANE_KB), dim3(256), 0, stream, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return (int)st;
     // Two waves per SIMD and 256 rows when that still gives every CU a

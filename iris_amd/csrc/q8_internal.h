@@ -108,7 +108,7 @@ struct GemvArgs {
     // Multi-token products of row-scale matrices go through the int8 MFMA
     // GEMM when this work space is given (null: the GEMV path).
     int8_t* planes;             // gemm_planes_bytes(cols, tokens): 5 digit planes, MFMA-operand tiled
-    int32_t* token_limbs;       // [tokens]: digits each token's activations need
+    int32_t* token_limbs;       // [2][tokens]: digits each token's activations need, then its rms_norm scale
 };
 
 // Bytes of the MFMA product's digit planes: 5 planes of the tokens rounded
