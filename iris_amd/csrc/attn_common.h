@@ -116,8 +116,8 @@ __device__ inline void attend_row(const AttnArgs& a, uint32_t head, uint32_t tok
     // exp terms and their saturating sum (non-negative terms: order-free).
     int64_t part = 0;
     for (uint32_t j = tid; j < n; j += nthreads) {
-        const int64_t delta = (int64_t)dn::sub_sat(s_w[j], m.v) * 65536;
-        const int64_t e = dn::softmax_exp_term(delta);
+        const int64_t diff = (int64_t)m.v - s_w[j];  // >= 0: m is the maximum
+        const int64_t e = (int64_t)dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
         s_e[j] = e;
         part = dn::acc_add_sat(part, e);
     }
@@ -129,8 +129,9 @@ __device__ inline void attend_row(const AttnArgs& a, uint32_t head, uint32_t tok
 
     // weights requantize(div_acc(e, sum)) and their saturating sum.
     int32_t wpart = 0;
+    const double w_scale = 65536.0 / (double)total, q_scale = 4294967296.0 / (double)total;
     for (uint32_t j = tid; j < n; j += nthreads) {
-        const int32_t w = dn::requantize(dn::div_acc_softmax((uint64_t)s_e[j], (uint64_t)total));
+        const int32_t w = dn::softmax_weight_fast((uint64_t)s_e[j], (uint64_t)total, w_scale, q_scale);
         s_w[j] = w;
         wpart = dn::add_sat(wpart, w);
     }

@@ -130,29 +130,6 @@ __device__ inline int64_t nth_root_acc(int64_t value, uint32_t degree) {
     return (lower & 1) == 0 ? lower : upper;
 }
 
-// ops.rs:67-78 div_acc for the softmax's case: numerator in [0, 2^32] and
-// denominator >= numerator > 0, so the 96-bit dividend e * 2^32 <= 2^64 is
-// handled with one 64-bit division (the 2^64 edge by its predecessor).
-__device__ __forceinline__ int64_t div_acc_softmax(uint64_t e, uint64_t sum) {
-    uint64_t q, r;
-    if (e < ((uint64_t)1 << 32)) {
-        uint64_t d = e << 32;
-        q = d / sum;
-        r = d - q * sum;
-    } else {  // e == 2^32: dividend 2^64 = (2^64 - 1) + 1
-        uint64_t d = ~(uint64_t)0;
-        q = d / sum;
-        r = d - q * sum + 1;
-        if (r == sum) { q += 1; r = 0; }
-    }
-    if (r == 0) return (int64_t)q;
-    // twice-remainder against the divisor, without overflow
-    uint64_t other = sum - r;
-    if (r < other) return (int64_t)q;
-    if (r > other) return (int64_t)(q + 1);
-    return (q & 1) == 0 ? (int64_t)q : (int64_t)(q + 1);
-}
-
 // ops.rs:722-771. The reference binary-searches the largest r in
 // [0, i32::MAX] with r*r*x <= 2^64; that r is found here from a double
 // estimate corrected with the same exact u128 test (the test is monotone in
@@ -218,28 +195,6 @@ __device__ __forceinline__ int64_t div_nonneg_by_u32(int64_t value, uint32_t n) 
 __device__ __forceinline__ int32_t rms_scale_from_sum(int64_t sum_squares, uint32_t n, int64_t eps) {
     int64_t mean = div_nonneg_by_u32(sum_squares, n);
     return inv_sqrt_acc(acc_add_sat(mean, eps));
-}
-
-// ops.rs:508-556
-__device__ inline int64_t softmax_exp_term(int64_t delta) {
-    const int64_t LN_2_BITS = 2977044472LL;
-    const int64_t MIN_DELTA = -((int64_t)16 << 32);
-    if (delta <= MIN_DELTA) return 0;
-    int64_t positive = sat_neg_i64(delta);
-    int64_t shift = positive / LN_2_BITS;
-    int64_t r = positive % LN_2_BITS;
-    int64_t r2 = acc_mul(r, r);
-    int64_t r3 = acc_mul(r2, r);
-    int64_t r4 = acc_mul(r3, r);
-    int64_t r5 = acc_mul(r4, r);
-    int64_t approx = acc_add_sat(
-        acc_add_sat(ONE_ACC, sat_neg_i64(r)),
-        acc_add_sat(div_acc_by_u32(r2, 2),
-                    acc_add_sat(sat_neg_i64(div_acc_by_u32(r3, 6)),
-                                acc_add_sat(div_acc_by_u32(r4, 24), sat_neg_i64(div_acc_by_u32(r5, 120))))));
-    if (approx <= 0) return 0;
-    if (shift < 64) return rshift_rte(approx, (uint32_t)shift);
-    return 0;
 }
 
 // rte(x / c) (ops.rs:691-720) for a non-negative dividend below 2^32.

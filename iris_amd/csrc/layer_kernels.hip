@@ -129,7 +129,8 @@ __global__ __launch_bounds__(512) void attn_chunk_softmax_pv_kernel(const AttnAr
     for (uint32_t u = 0; u < SPT; u++) {
         const uint32_t j = tid + u * NT;
         if (j < n) {
-            const int64_t e = dn::softmax_exp_term((int64_t)dn::sub_sat(sv[u], m.v) * 65536);
+            const int64_t diff = (int64_t)m.v - sv[u];  // >= 0: m is the maximum
+            const int64_t e = (int64_t)dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
             part = dn::acc_add_sat(part, e);
             if (j >= c0 && j < c0 + cn) s_e[j - c0] = e;
         }
@@ -143,7 +144,8 @@ __global__ __launch_bounds__(512) void attn_chunk_softmax_pv_kernel(const AttnAr
     // 4. This chunk's weights and their saturating sum.
     int32_t wpart = 0;
     if (tid < cn) {
-        const int32_t w = dn::requantize(dn::div_acc_softmax((uint64_t)s_e[tid], (uint64_t)total));
+        const int32_t w = dn::softmax_weight_fast((uint64_t)s_e[tid], (uint64_t)total, 65536.0 / (double)total,
+                                                  4294967296.0 / (double)total);
         s_w[tid] = w;
         wpart = w;
         if (c0 + tid == m.i) a.max_weight[head] = w;
