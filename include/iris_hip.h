@@ -217,6 +217,11 @@ int iris_attention_numerics(const uint32_t* diff, const uint64_t* e, const uint6
                             uint32_t scale_q32, uint32_t n, uint64_t* exp_out, int32_t* weight_out,
                             int32_t* score_out);
 
+/* Numerics check: silu (crates/det-num/src/mistral.rs:59-77, the SwiGLU
+ * gate) of n Q16.16 values on the device, as the product epilogues compute
+ * it (device pointers; synchronous). No counterpart in the reference. */
+int iris_silu_device(const int32_t* x, uint32_t n, int32_t* out);
+
 /* SHA-256 (FIPS 180-4) of `len` bytes into out[32]; the hash
  * iris_session_layer_pass uses. Host code only. */
 int iris_sha256_bytes(const uint8_t* data, uint64_t len, uint8_t* out);

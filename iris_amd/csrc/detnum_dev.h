@@ -357,16 +357,32 @@ __device__ __forceinline__ int64_t m_shift_rte(int64_t value, uint32_t shift) {
     return (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
 }
 
-// mistral.rs:43-56
+// mistral.rs:43-56. r < ln 2 < 2^32 and acc <= 2^32 throughout, so each
+// Horner step's (r * acc) >> 32 is one 32 x 32-bit product (r itself while
+// acc is exactly 2^32), and its quotient by n a 32-bit one.
 __device__ inline uint64_t exp_neg_q32(uint64_t a) {
     const uint64_t ONE_Q32 = (uint64_t)1 << 32, LN2 = 2977044472ULL;
-    uint64_t k = a / LN2;
+    const uint64_t k = a / LN2;
     if (k >= 32) return 0;
-    uint64_t r = a - k * LN2;
+    const uint32_t r = (uint32_t)(a - k * LN2);
     uint64_t acc = ONE_Q32;
 #pragma unroll
-    for (uint32_t n = 14; n >= 1; n--) acc = ONE_Q32 - ((r * acc) >> 32) / n;
+    for (uint32_t n = 14; n >= 1; n--) {
+        const uint32_t prod = acc == ONE_Q32 ? r : (uint32_t)(((uint64_t)r * (uint32_t)acc) >> 32);
+        acc = ONE_Q32 - prod / n;
+    }
     return acc >> k;
+}
+
+// floor(2^63 / d) for 2^32 <= d <= 2^33: a double estimate (within 2^-22 of
+// the quotient, so its floor is off by at most one) corrected on the exact
+// remainder.
+__device__ __forceinline__ uint64_t floor_2p63_over(uint64_t d) {
+    uint64_t q = (uint64_t)(9223372036854775808.0 / (double)d);
+    const int64_t rem = (int64_t)(((uint64_t)1 << 63) - q * d);
+    if (rem < 0) q--;
+    else if ((uint64_t)rem >= d) q++;
+    return q;
 }
 
 // mistral.rs:59-77
@@ -374,7 +390,7 @@ __device__ inline int32_t silu(int32_t x) {
     const uint64_t ONE_Q32 = (uint64_t)1 << 32;
     uint64_t mag = x < 0 ? (uint64_t)(-(int64_t)x) : (uint64_t)x;
     uint64_t divisor = ONE_Q32 + exp_neg_q32(mag << 16);
-    uint64_t positive = (((uint64_t)1 << 63) / divisor) << 1;
+    uint64_t positive = floor_2p63_over(divisor) << 1;
     uint64_t sig = x < 0 ? ONE_Q32 - positive : positive;
     int64_t product = (int64_t)x * (int64_t)sig;
     return clamp_i64_to_i32(m_shift_rte(product, 32));
@@ -419,6 +435,13 @@ __device__ inline void sin_cos_q30(int64_t angle, int64_t& sin_out, int64_t& cos
 __device__ __forceinline__ void rotate_pair_q30(int32_t& a, int32_t& b, int64_t angle) {
     int64_t s, c;
     sin_cos_q30(angle, s, c);
+    int64_t x = a, y = b;
+    a = clamp_i64_to_i32(m_shift_rte(x * c - y * s, 30));
+    b = clamp_i64_to_i32(m_shift_rte(x * s + y * c, 30));
+}
+
+// The same rotation with (sin, cos) already formed.
+__device__ __forceinline__ void rotate_pair_sc(int32_t& a, int32_t& b, int64_t s, int64_t c) {
     int64_t x = a, y = b;
     a = clamp_i64_to_i32(m_shift_rte(x * c - y * s, 30));
     b = clamp_i64_to_i32(m_shift_rte(x * s + y * c, 30));

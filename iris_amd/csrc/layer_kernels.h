@@ -124,4 +124,8 @@ int iris_norm_residual_launch(const int32_t* a, uint32_t a_stride, const int32_t
                               uint32_t rows, hipStream_t stream);
 int iris_i32_gemv_launch(const I32GemvArgs& a, uint32_t tokens, hipStream_t stream);
 int iris_ple_prepare_launch(const PleArgs& a, uint32_t segments, uint32_t rows, hipStream_t stream);
+// (sin, cos) in Q30 (mistral.rs:84-109) of position * inv_freq[j] for the
+// `rows` positions from *d_pos and j < half: out[row][j][2].
+int iris_rope_table_launch(const int64_t* inv_freq, uint32_t half, const int32_t* d_pos, uint32_t rows, int64_t* out,
+                           hipStream_t stream);
 int iris_rope_ladder_launch(int64_t base, uint32_t freq_base_dim, uint32_t half, int64_t* out, hipStream_t stream);

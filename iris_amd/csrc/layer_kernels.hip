@@ -259,7 +259,40 @@ __global__ void embed_rows_kernel(const int32_t* ids, const uint8_t* embed_raw, 
               blockDim.x);
 }
 
+__global__ __launch_bounds__(256) void rope_table_kernel(const int64_t* inv_freq, uint32_t half, const int32_t* d_pos,
+                                                         uint32_t rows, int64_t* out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * half) return;
+    const uint32_t row = i / half, j = i % half;
+    int64_t s, c;
+    dn::sin_cos_q30((int64_t)((uint32_t)(*d_pos) + row) * inv_freq[j], s, c);
+    out[2 * (size_t)i] = s;
+    out[2 * (size_t)i + 1] = c;
+}
+
+__global__ __launch_bounds__(256) void silu_kernel(const int32_t* x, uint32_t n, int32_t* out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = dn::silu(x[i]);
+}
+
 }  // namespace
+
+extern "C" int iris_silu_device(const int32_t* d_x, uint32_t n, int32_t* d_out) {
+    if (n == 0) return 0;
+    if (!d_x || !d_out) return IRIS_E_INVALID;
+    hipLaunchKernelGGL(silu_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, d_x, n, d_out);
+    hipError_t st = hipGetLastError();
+    if (st == hipSuccess) st = hipDeviceSynchronize();
+    return (int)st;
+}
+
+int iris_rope_table_launch(const int64_t* inv_freq, uint32_t half, const int32_t* d_pos, uint32_t rows, int64_t* out,
+                           hipStream_t stream) {
+    if (rows == 0 || half == 0) return 0;
+    hipLaunchKernelGGL(rope_table_kernel, dim3((rows * half + 255) / 256), dim3(256), 0, stream, inv_freq, half, d_pos,
+                       rows, out);
+    return (int)hipGetLastError();
+}
 
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream) {
     if (a.head_dim > ATTN_MAX_HEAD_DIM || a.head_dim % 4 || max_keys > ATTN_MAX_KEYS || a.heads % a.kv_heads)

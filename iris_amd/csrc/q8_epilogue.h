@@ -29,7 +29,15 @@ __device__ __forceinline__ void store_output(const GemvArgs& a, uint32_t row, ui
                 if ((row & 1) == 0) {
                     int32_t x0 = v, x1 = partner;
                     // mistral.rs:114-126: pair j of each head, position * f_j.
-                    if (pos != 0) dn::rotate_pair_q30(x0, x1, (int64_t)pos * a.inv_freq[(row % a.head_dim) >> 1]);
+                    const uint32_t j = (row % a.head_dim) >> 1;
+                    if (pos != 0) {
+                        if (a.rope_sc) {
+                            const int64_t* sc = a.rope_sc + ((size_t)token * (a.head_dim >> 1) + j) * 2;
+                            dn::rotate_pair_sc(x0, x1, sc[0], sc[1]);
+                        } else {
+                            dn::rotate_pair_q30(x0, x1, (int64_t)pos * a.inv_freq[j]);
+                        }
+                    }
                     if (row < a.q_rows) {
                         a.out[(size_t)token * a.out_stride + row] = x0;
                         a.out[(size_t)token * a.out_stride + row + 1] = x1;

@@ -89,6 +89,7 @@ struct GemvArgs {
     // EPI_ROPE_KV
     const int32_t* d_pos;       // absolute position of token 0 of this launch
     const int64_t* inv_freq;    // head_dim/2 Q32.32 angles per position
+    const int64_t* rope_sc;     // nullable: [tokens][head_dim/2][sin, cos] Q30 for these positions
     uint32_t head_dim, q_rows, kv_rows;
     int32_t* k_cache;           // transposed: [kv_rows][k_pos_stride]
     uint32_t k_pos_stride;

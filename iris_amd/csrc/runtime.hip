@@ -411,6 +411,8 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     const uint32_t H = d.hidden;
     const uint32_t qw = d.heads * d.head_dim, kvw = d.kv_heads * d.head_dim;
     hipStream_t st = s->stream;
+    // The rows' RoPE (sin, cos) pairs, shared by every layer.
+    RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, st));
     for (uint32_t l = 0; l < d.layers; l++) {
         const LayerWeights& L = m->layers[l];
         GemvArgs g{};
@@ -427,6 +429,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.out_stride = qw;
         g.d_pos = s->d_pos;
         g.inv_freq = m->inv_freq;
+        g.rope_sc = s->rope_sc;
         g.head_dim = d.head_dim;
         g.q_rows = qw;
         g.kv_rows = kvw;
@@ -766,6 +769,8 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     auto alloc = [&](int32_t** p, size_t n) {
         if (st == hipSuccess) st = hipMalloc((void**)p, (n ? n : 1) * 4);
     };
+    if (d.family != IRIS_FAMILY_GEMMA_DENSE && st == hipSuccess)
+        st = hipMalloc((void**)&s->rope_sc, (size_t)max_rows * d.head_dim * sizeof(int64_t));
     alloc(&s->x, (size_t)max_rows * d.hidden);
     alloc(&s->attended, (size_t)max_rows * d.hidden);
     alloc(&s->q, (size_t)max_rows * qw);
@@ -839,6 +844,7 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->attn_planes.q_limbs);
     hipFree(s->attn_planes.kv_limbs);
     hipFree(s->attn_planes.e_store);
+    hipFree(s->rope_sc);
     hipFree(s->ckpt_dev);
     if (s->ckpt_host) hipHostFree(s->ckpt_host);
     for (auto e : s->ckpt_events)

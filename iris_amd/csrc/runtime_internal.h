@@ -85,6 +85,7 @@ struct IrisSession {
     int64_t* attn_chunk_acc = nullptr;
     int32_t* attn_chunk_wsum = nullptr;
     int32_t* attn_max_weight = nullptr;
+    int64_t* rope_sc = nullptr;      // mistral-dense: [max_rows][head_dim/2][sin, cos] of the pass's positions
     // multi-row attention digit planes (null for single-row sessions)
     AttnPlanes attn_planes{};
     // per-layer checkpoint staging, made on the first checkpointing pass

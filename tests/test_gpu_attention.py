@@ -111,3 +111,20 @@ def test_prefill_attention_gemma_sliding_window():
     m = synth.gemma_model(shape, 512, seed=5)
     _check_pass(m, 100)
     _check_pass(synth.tiny_gemma(), 33)
+
+
+def test_silu_against_oracle():
+    # The SwiGLU gate as the product epilogues compute it (narrow Horner
+    # steps, the 2^63 quotient from a corrected double estimate): every value
+    # in [-2^20, 2^20] in steps of 3, the ends of the range and random values.
+    O = cpu.lib()
+    rng = np.random.default_rng(9)
+    x = np.concatenate([np.arange(-(1 << 20), (1 << 20) + 1, 3, dtype=np.int64),
+                        np.array([0, 1, -1, 2 ** 31 - 1, -2 ** 31, 2 ** 31 - 2, -2 ** 31 + 1]),
+                        rng.integers(-2 ** 31, 2 ** 31, 300000)]).astype(np.int32)
+    dx = native.DeviceBuffer.from_array(x)
+    dout = native.DeviceBuffer(4 * x.size)
+    native.check(native.lib().iris_silu_device(dx.ptr, x.size, dout.ptr), "silu")
+    got = dout.to_array(np.int32, (x.size,))
+    want = np.array([O.dn_silu(int(v)) for v in x], np.int32)
+    assert np.array_equal(got, want)
