@@ -237,8 +237,9 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
 }
 
 // Output e of lane l of a 32 x 32 block is row 8(e/4) + 4(l/32) + e%4,
-// token l % 32: recombine the planes, scale, round once, park the block in
-// LDS as [row][token], then run the epilogue row-fastest.
+// token l % 32: recombine the planes, scale, round once (and, for the
+// gated activations, combine each gate/up row pair in registers), park the
+// block in LDS as [row][token], then run the epilogue row-fastest.
 template <class G, int LG, int TTW>
 __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
                                               const v16i (&acc)[2][TTW][LG]) {
@@ -247,29 +248,53 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t wr = wave % (G::WAVES / 2), wt = wave / (G::WAVES / 2);
     const Q8View& w = a.w;
+    const bool pairs = a.epilogue == EPI_SWIGLU || a.epilogue == EPI_GEGLU;
     int32_t* sC = (int32_t*)smem;
 #pragma unroll
     for (int i = 0; i < 2; i++) {
 #pragma unroll
         for (int j = 0; j < TTW; j++) {
             const uint32_t tl = (wt * TTW + j) * 32 + (lane & 31);
+            int32_t v[16];
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4), row = rt0 * 32 + rl;
                 int64_t tot = 0;  // the row's integer dot product, |tot| < K * 2^38
 #pragma unroll
                 for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
-                sC[rl * STRIDE + tl] =
-                    row < w.rows ? dn::round_to_i32((dn::i128)tot * (dn::i128)w.row_scale[row], 24) : 0;
+                v[e] = row < w.rows ? dn::round_to_i32((dn::i128)tot * (dn::i128)w.row_scale[row], 24) : 0;
+            }
+            if (pairs) {
+                // Rows e and e + 1 (e even) are a gate/up pair in this lane:
+                // the activation runs here, once per pair, every lane busy.
+#pragma unroll
+                for (int e = 0; e < 16; e += 2) {
+                    const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                    const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v[e]) : dn::gelu(v[e]);
+                    sC[(rl >> 1) * STRIDE + tl] = dn::mul_sat(act, v[e + 1]);
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 16; e++)
+                    sC[((wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4)) * STRIDE + tl] = v[e];
             }
         }
     }
     __syncthreads();
-    for (uint32_t c = tid; c < ROWS * NTOK; c += G::THREADS) {
-        const uint32_t rl = c % ROWS, tl = c / ROWS;
-        const uint32_t row = rt0 * 32 + rl, token = tt0 * 32 + tl;
-        if (row < w.rows && token < a.tokens)
-            store_output(a, row, token, sC[rl * STRIDE + tl], sC[(rl ^ 1) * STRIDE + tl]);
+    if (pairs) {
+        // out[token][row / 2] for the block's ROWS / 2 pairs.
+        for (uint32_t c = tid; c < ROWS / 2 * NTOK; c += G::THREADS) {
+            const uint32_t pl = c % (ROWS / 2), tl = c / (ROWS / 2);
+            const uint32_t pair = rt0 * 16 + pl, token = tt0 * 32 + tl;
+            if (2 * pair < w.rows && token < a.tokens) a.out[(size_t)token * a.out_stride + pair] = sC[pl * STRIDE + tl];
+        }
+    } else {
+        for (uint32_t c = tid; c < ROWS * NTOK; c += G::THREADS) {
+            const uint32_t rl = c % ROWS, tl = c / ROWS;
+            const uint32_t row = rt0 * 32 + rl, token = tt0 * 32 + tl;
+            if (row < w.rows && token < a.tokens)
+                store_output(a, row, token, sC[rl * STRIDE + tl], sC[(rl ^ 1) * STRIDE + tl]);
+        }
     }
     __syncthreads();
 }
