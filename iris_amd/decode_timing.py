@@ -171,6 +171,20 @@ def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None) -> dict:
     return r
 
 
+def trace_decode(steps: int = 64) -> dict:
+    """A short decode for kernel traces: a session of 1024 positions, a
+    512-token prompt (ids from seed 1), `steps` greedy steps replayed as a
+    HIP graph, timed with HIP events; nothing else runs."""
+    model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
+    dm = DeviceModel(model)
+    del model.tensors
+    session = Session(dm, 1024, PROMPT)
+    ms, prefill, _ = session.time_decode(synth.token_ids(1, PROMPT, 32000), steps)
+    session.free()
+    dm.free()
+    return {"decode_ms_per_step": round(ms, 4), "prompt_pass_ms": round(prefill, 2), "steps": steps}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
     ap.add_argument("--steps", type=int, default=PROMPT - 1)
@@ -181,8 +195,13 @@ def main(argv=None):
     ap.add_argument("--pass-rows", type=int, default=0,
                     help="time only the teacher-forced pass over this many rows")
     ap.add_argument("--gemm-only", action="store_true", help="time only the MFMA product at the gate|up shape")
+    ap.add_argument("--trace-decode", type=int, default=0, metavar="STEPS",
+                    help="only a short decode of STEPS steps (for kernel traces)")
     args = ap.parse_args(argv)
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    if args.trace_decode:
+        print(json.dumps(trace_decode(args.trace_decode)), flush=True)
+        return
     if args.gemm_only:
         print(json.dumps(time_gemm()), flush=True)
         return
