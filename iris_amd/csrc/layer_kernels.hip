@@ -238,6 +238,154 @@ int attention_split_launch(const AttnArgs& a, uint32_t chunks, hipStream_t strea
     return (int)hipGetLastError();
 }
 
+// One query row in one launch. Every workgroup of a head recomputes the
+// head's scores (thread pairs split a key's dimensions; the key loads of up
+// to 256 * RB keys are issued together), its first maximum, exp terms and
+// weights, then forms the weighted values of its own 32-dimension slice over
+// every key, the slice's value loads issued before the softmax so they are
+// in flight while it runs. No partials cross workgroups: nothing to combine.
+template <uint32_t HD>
+__global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
+    constexpr uint32_t NT = 512, NWV = NT / 64, HALF = HD / 2;
+    constexpr uint32_t RB = HALF >= 128 ? 1 : 128 / HALF;  // 256-key rounds of key loads in flight together
+    constexpr uint32_t DS = 32;                             // dimensions per workgroup
+    constexpr uint32_t VR = 16;                             // 64-key value rounds loaded before the softmax
+    constexpr uint32_t EPT = ATTN_MAX_KEYS / NT;            // exp terms per thread, at most
+    __shared__ int32_t s_w[ATTN_MAX_KEYS];                  // scores, then weights
+    __shared__ int32_t s_q[HD];
+    __shared__ int64_t s_part[64 * DS];
+    __shared__ ArgMax s_am[NWV];
+    __shared__ uint64_t s_sum[NWV];
+    __shared__ int32_t s_wsum[NWV];
+    const uint32_t head = blockIdx.x, slice = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t kvh = head / (a.heads / a.kv_heads);
+    const uint32_t pos = (uint32_t)(*a.d_pos);
+    const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
+    const uint32_t n = pos - start + 1;
+    for (uint32_t d = tid; d < HD; d += NT) s_q[d] = a.q[(size_t)head * HD + d];
+    __syncthreads();
+
+    // 1. Scores (wrapping i64 dot, then scaled_score or requantize) and the
+    // first maximum; keys run in increasing order in each thread.
+    const uint32_t half = (lane >> 5) & 1, kl = wave * 32 + (lane & 31);
+    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + half * HALF) * a.k_pos_stride + start;
+    ArgMax best{INT32_MIN, 0xffffffffu};
+    for (uint32_t k0 = 0; k0 < n; k0 += 256 * RB) {
+        int32_t kv[RB][HALF];
+#pragma unroll
+        for (uint32_t r = 0; r < RB; r++) {
+            const uint32_t key = k0 + 256 * r + kl, safe = key < n ? key : 0;
+#pragma unroll
+            for (uint32_t i = 0; i < HALF; i++) kv[r][i] = kb[(size_t)i * a.k_pos_stride + safe];
+        }
+#pragma unroll
+        for (uint32_t r = 0; r < RB; r++) {
+            const uint32_t key = k0 + 256 * r + kl;
+            uint64_t dot = 0;
+#pragma unroll
+            for (uint32_t i = 0; i < HALF; i++) dot += (uint64_t)((int64_t)s_q[half * HALF + i] * kv[r][i]);
+            dot += __shfl_xor(dot, 32);
+            if (half == 0 && key < n) {
+                const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)dot, a.scale_q32)
+                                            : dn::requantize((int64_t)dot);
+                s_w[key] = sc;
+                if (sc > best.v) best = ArgMax{sc, key};
+            }
+        }
+    }
+    best = wave_argmax(best);
+    if (lane == 0) s_am[wave] = best;
+
+    // 2. This slice's value rows, loaded now, used after the softmax.
+    const uint32_t kr = tid / 8, d4 = (tid % 8) * 4;
+    const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * HD + slice * DS + d4;
+    int4 vv[VR];
+#pragma unroll
+    for (uint32_t r = 0; r < VR; r++) {
+        const uint32_t key = kr + 64 * r;
+        vv[r] = *(const int4*)(vb + (size_t)(key < n ? key : 0) * a.kv_stride);
+    }
+    __syncthreads();
+    ArgMax m = s_am[0];
+    for (uint32_t i = 1; i < NWV; i++) m = argmax_combine(m, s_am[i]);
+
+    // 3. Exp terms (non-negative: their sum is order-free and cannot
+    // saturate for 4096 keys) and 4. the weights and their sum.
+    uint64_t ev[EPT];
+    uint64_t part = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < EPT; u++) {
+        const uint32_t j = tid + NT * u;
+        ev[u] = 0;
+        if (j < n) {
+            const int64_t diff = (int64_t)m.v - s_w[j];
+            ev[u] = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
+        }
+        part += ev[u];
+    }
+    for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+    if (lane == 0) s_sum[wave] = part;
+    __syncthreads();
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < NWV; i++) total += s_sum[i];
+    const double w_scale = 65536.0 / (double)total, q_scale = 4294967296.0 / (double)total;
+    int32_t wpart = 0;
+#pragma unroll
+    for (uint32_t u = 0; u < EPT; u++) {
+        const uint32_t j = tid + NT * u;
+        if (j < n) {
+            const int32_t w = dn::softmax_weight_fast(ev[u], total, w_scale, q_scale);
+            s_w[j] = w;
+            wpart += w;
+        }
+    }
+    wpart = wave_sum_sat32(wpart);
+    if (lane == 0) s_wsum[wave] = wpart;
+    __syncthreads();
+    int32_t wsum = 0;
+    for (uint32_t i = 0; i < NWV; i++) wsum = dn::add_sat(wsum, s_wsum[i]);
+
+    // 5. Weighted values of the slice (wrapping i64), 64 key rows in parallel.
+    uint64_t acc[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (uint32_t r = 0; r < VR; r++) {
+        const uint32_t key = kr + 64 * r;
+        if (key < n) {
+            const int64_t w = s_w[key];
+            acc[0] += (uint64_t)(w * vv[r].x);
+            acc[1] += (uint64_t)(w * vv[r].y);
+            acc[2] += (uint64_t)(w * vv[r].z);
+            acc[3] += (uint64_t)(w * vv[r].w);
+        }
+    }
+    for (uint32_t key = kr + 64 * VR; key < n; key += 64) {
+        const int4 v = *(const int4*)(vb + (size_t)key * a.kv_stride);
+        const int64_t w = s_w[key];
+        acc[0] += (uint64_t)(w * v.x);
+        acc[1] += (uint64_t)(w * v.y);
+        acc[2] += (uint64_t)(w * v.z);
+        acc[3] += (uint64_t)(w * v.w);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) s_part[kr * DS + d4 + c] = (int64_t)acc[c];
+    __syncthreads();
+    if (tid < DS) {
+        uint64_t t = 0;
+        for (uint32_t r = 0; r < 64; r++) t += (uint64_t)s_part[r * DS + tid];
+        // The first maximum's weight w becomes add_sat(w, ONE - sum): no
+        // saturation for these magnitudes, so the change is + (ONE - sum) * v.
+        const int64_t resid = dn::sub_sat(dn::ONE_ACT, wsum);
+        t += (uint64_t)(resid * a.v_cache[(size_t)(start + m.i) * a.kv_stride + (size_t)kvh * HD + slice * DS + tid]);
+        a.ctx[(size_t)head * HD + slice * DS + tid] = dn::requantize((int64_t)t);
+    }
+}
+
+template <uint32_t HD>
+int attention_decode_launch(const AttnArgs& a, hipStream_t stream) {
+    hipLaunchKernelGGL(attn_decode_kernel<HD>, dim3(a.heads, HD / 32), dim3(512), 0, stream, a);
+    return (int)hipGetLastError();
+}
+
 // Dequantize one Q8_0 row (reference layout) into out[0..cols) (q8.rs:76-92),
 // optionally times a Q16.16 scale (model.rs:316-330).
 __device__ __forceinline__ void embed_row(const uint8_t* row, uint32_t cols, int32_t scale, int32_t* out,
@@ -300,11 +448,12 @@ int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys,
     if (tokens == 1 && a.scores) {
         // One row: every head over chunks of keys, in three launches.
         const uint32_t chunks = (max_keys + ATTN_CHUNK - 1) / ATTN_CHUNK;
+        (void)chunks;
         switch (a.head_dim) {
-            case 32: return attention_split_launch<32>(a, chunks, stream);
-            case 64: return attention_split_launch<64>(a, chunks, stream);
-            case 128: return attention_split_launch<128>(a, chunks, stream);
-            case 256: return attention_split_launch<256>(a, chunks, stream);
+            case 32: return attention_decode_launch<32>(a, stream);
+            case 64: return attention_decode_launch<64>(a, stream);
+            case 128: return attention_decode_launch<128>(a, stream);
+            case 256: return attention_decode_launch<256>(a, stream);
             default: break;  // other head sizes: the one-workgroup-per-head kernel
         }
     }
