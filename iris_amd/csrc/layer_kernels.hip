@@ -239,15 +239,14 @@ int attention_split_launch(const AttnArgs& a, uint32_t chunks, hipStream_t strea
 }
 
 // One query row in one launch. Every workgroup of a head recomputes the
-// head's scores (thread pairs split a key's dimensions; the key loads of up
-// to 256 * RB keys are issued together), its first maximum, exp terms and
+// head's scores (the key loads of a round issued together), its first
+// maximum, exp terms and
 // weights, then forms the weighted values of its own 32-dimension slice over
 // every key, the slice's value loads issued before the softmax so they are
 // in flight while it runs. No partials cross workgroups: nothing to combine.
 template <uint32_t HD>
 __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
-    constexpr uint32_t NT = 512, NWV = NT / 64, HALF = HD / 2;
-    constexpr uint32_t RB = HALF >= 128 ? 1 : 128 / HALF;  // 256-key rounds of key loads in flight together
+    constexpr uint32_t NT = 512, NWV = NT / 64;
     constexpr uint32_t DS = 32;                             // dimensions per workgroup
     constexpr uint32_t VR = 16;                             // 64-key value rounds loaded before the softmax
     constexpr uint32_t EPT = ATTN_MAX_KEYS / NT;            // exp terms per thread, at most
@@ -266,30 +265,47 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     __syncthreads();
 
     // 1. Scores (wrapping i64 dot, then scaled_score or requantize) and the
-    // first maximum; keys run in increasing order in each thread.
-    const uint32_t half = (lane >> 5) & 1, kl = wave * 32 + (lane & 31);
-    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + half * HALF) * a.k_pos_stride + start;
+    // first maximum. Thread (dimension group g of NDG, key quad kq) holds the
+    // 32 dimensions 32g.. of four consecutive positions, one 16-byte load per
+    // dimension from the transposed cache (its position stride is a multiple
+    // of 64; consecutive lanes read consecutive positions of one dimension);
+    // the groups' partial sums meet by shuffles. Positions run in increasing
+    // order in each thread.
+    constexpr uint32_t NDG = HD / 32, QPW = 64 / NDG, KPR = 4 * QPW * NWV;  // positions per round
+    const uint32_t g = lane / QPW, kq = wave * QPW + lane % QPW;
+    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + 32 * g) * a.k_pos_stride;
+    const uint32_t p0 = start & ~3u;
     ArgMax best{INT32_MIN, 0xffffffffu};
-    for (uint32_t k0 = 0; k0 < n; k0 += 256 * RB) {
-        int32_t kv[RB][HALF];
+    for (uint32_t pb = p0; pb <= pos; pb += KPR) {
+        const uint32_t p = pb + 4 * kq, safe = p <= pos ? p : p0;
+        int4 kv[32];
 #pragma unroll
-        for (uint32_t r = 0; r < RB; r++) {
-            const uint32_t key = k0 + 256 * r + kl, safe = key < n ? key : 0;
+        for (uint32_t i = 0; i < 32; i++) kv[i] = *(const int4*)(kb + (size_t)i * a.k_pos_stride + safe);
+        uint64_t dot[4] = {0, 0, 0, 0};
 #pragma unroll
-            for (uint32_t i = 0; i < HALF; i++) kv[r][i] = kb[(size_t)i * a.k_pos_stride + safe];
+        for (uint32_t i = 0; i < 32; i++) {
+            const int64_t q = s_q[32 * g + i];
+            dot[0] += (uint64_t)(q * kv[i].x);
+            dot[1] += (uint64_t)(q * kv[i].y);
+            dot[2] += (uint64_t)(q * kv[i].z);
+            dot[3] += (uint64_t)(q * kv[i].w);
         }
 #pragma unroll
-        for (uint32_t r = 0; r < RB; r++) {
-            const uint32_t key = k0 + 256 * r + kl;
-            uint64_t dot = 0;
+        for (uint32_t off = QPW; off < 64; off <<= 1)
 #pragma unroll
-            for (uint32_t i = 0; i < HALF; i++) dot += (uint64_t)((int64_t)s_q[half * HALF + i] * kv[r][i]);
-            dot += __shfl_xor(dot, 32);
-            if (half == 0 && key < n) {
-                const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)dot, a.scale_q32)
-                                            : dn::requantize((int64_t)dot);
+            for (int c = 0; c < 4; c++) dot[c] += __shfl_xor(dot[c], off);
+        // Every group holds the four sums now; group g scores positions
+        // CPL*g.. of the quad.
+        constexpr uint32_t CPL = NDG >= 4 ? 1 : 4 / NDG;
+#pragma unroll
+        for (uint32_t c = 0; c < 4; c++) {
+            const uint32_t at = p + c;
+            if (c / CPL == g && at >= start && at <= pos) {
+                const uint32_t key = at - start;
+                const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)dot[c], a.scale_q32)
+                                            : dn::requantize((int64_t)dot[c]);
                 s_w[key] = sc;
-                if (sc > best.v) best = ArgMax{sc, key};
+                best = argmax_combine(best, ArgMax{sc, key});
             }
         }
     }
@@ -445,10 +461,8 @@ int iris_rope_table_launch(const int64_t* inv_freq, uint32_t half, const int32_t
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream) {
     if (a.head_dim > ATTN_MAX_HEAD_DIM || a.head_dim % 4 || max_keys > ATTN_MAX_KEYS || a.heads % a.kv_heads)
         return IRIS_E_INVALID;
-    if (tokens == 1 && a.scores) {
-        // One row: every head over chunks of keys, in three launches.
-        const uint32_t chunks = (max_keys + ATTN_CHUNK - 1) / ATTN_CHUNK;
-        (void)chunks;
+    if (tokens == 1 && a.k_pos_stride % 4 == 0) {
+        // One row: HD/32 workgroups per head, each over every key.
         switch (a.head_dim) {
             case 32: return attention_decode_launch<32>(a, stream);
             case 64: return attention_decode_launch<64>(a, stream);

@@ -53,24 +53,54 @@ __device__ __forceinline__ dn::i128 kgroup_sum(dn::i128 v) {
     return v;
 }
 
-template <int L>
-__device__ __forceinline__ int64_t block_sum_pw(const uint4 q0, const uint4 q1, const uint32_t* lb, uint32_t pw) {
+// Planes l0 .. l0+N-1 of one block's sum: their 16-byte LDS reads are all
+// issued before the first dot product, and each plane's sum is two
+// independent chains (|half| < 2^18, so the i32 sums are exact).
+template <int L0, int N>
+__device__ __forceinline__ int64_t plane_sums(const uint4 q0, const uint4 q1, const uint32_t* lb, uint32_t pw) {
+    uint4 p[N][2];
+#pragma unroll
+    for (int l = 0; l < N; l++) {
+        p[l][0] = *(const uint4*)(lb + (L0 + l) * pw);
+        p[l][1] = *(const uint4*)(lb + (L0 + l) * pw + 4);
+    }
     int64_t bs = 0;
 #pragma unroll
-    for (int l = 0; l < L; l++) {
-        const uint32_t* p = lb + l * pw;
-        int s = 0;
-        s = __builtin_amdgcn_sdot4((int)q0.x, (int)p[0], s, false);
-        s = __builtin_amdgcn_sdot4((int)q0.y, (int)p[1], s, false);
-        s = __builtin_amdgcn_sdot4((int)q0.z, (int)p[2], s, false);
-        s = __builtin_amdgcn_sdot4((int)q0.w, (int)p[3], s, false);
-        s = __builtin_amdgcn_sdot4((int)q1.x, (int)p[4], s, false);
-        s = __builtin_amdgcn_sdot4((int)q1.y, (int)p[5], s, false);
-        s = __builtin_amdgcn_sdot4((int)q1.z, (int)p[6], s, false);
-        s = __builtin_amdgcn_sdot4((int)q1.w, (int)p[7], s, false);
-        bs += (int64_t)s << (8 * l);
+    for (int l = 0; l < N; l++) {
+        int s0 = 0, s1 = 0;
+        s0 = __builtin_amdgcn_sdot4((int)q0.x, (int)p[l][0].x, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)q1.x, (int)p[l][1].x, s1, false);
+        s0 = __builtin_amdgcn_sdot4((int)q0.y, (int)p[l][0].y, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)q1.y, (int)p[l][1].y, s1, false);
+        s0 = __builtin_amdgcn_sdot4((int)q0.z, (int)p[l][0].z, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)q1.z, (int)p[l][1].z, s1, false);
+        s0 = __builtin_amdgcn_sdot4((int)q0.w, (int)p[l][0].w, s0, false);
+        s1 = __builtin_amdgcn_sdot4((int)q1.w, (int)p[l][1].w, s1, false);
+        bs += (int64_t)(s0 + s1) << (8 * (L0 + l));
     }
     return bs;
+}
+
+// Exact sum of one block's 32 int8 weights (q0: bytes 0-15, q1: 16-31)
+// times the values whose L digit planes start at lb (plane stride pw
+// dwords, 32-byte aligned), the planes read three at a time.
+template <int L>
+__device__ __forceinline__ int64_t block_sum_pw(const uint4 q0, const uint4 q1, const uint32_t* lb, uint32_t pw) {
+    if constexpr (L <= 3) return plane_sums<0, L>(q0, q1, lb, pw);
+    else return plane_sums<0, 3>(q0, q1, lb, pw) + plane_sums<3, L - 3>(q0, q1, lb, pw);
+}
+
+// block_sum_pw for a digit count that is uniform over the wave (held in a
+// scalar register): one scalar branch per block picks the unrolled body.
+__device__ __forceinline__ int64_t block_sum_planes(const uint4 q0, const uint4 q1, const uint32_t* lb, uint32_t pw,
+                                                    int L) {
+    switch (L) {
+        case 1: return block_sum_pw<1>(q0, q1, lb, pw);
+        case 2: return block_sum_pw<2>(q0, q1, lb, pw);
+        case 3: return block_sum_pw<3>(q0, q1, lb, pw);
+        case 4: return block_sum_pw<4>(q0, q1, lb, pw);
+        default: return block_sum_pw<5>(q0, q1, lb, pw);
+    }
 }
 
 // The blocks of one chunk this lane owns, accumulated into acc (i64 sum of
@@ -113,7 +143,7 @@ __device__ __forceinline__ void argmax_combine(int32_t& v, uint32_t& i, int32_t 
 // The head's epilogue, run by the wave finishing a tile: logits out
 // (softcapped) and the tile's first maximum to the partials; the selection
 // itself is the next kernel's (iris_select_launch).
-__device__ void head_select(const GemvArgs& a, int32_t v, uint32_t row, uint32_t lane, uint32_t tile) {
+__device__ __forceinline__ void head_select(const GemvArgs& a, int32_t v, uint32_t row, uint32_t lane, uint32_t tile) {
     const uint32_t step = (uint32_t)*a.d_step;
     int32_t best = INT32_MIN;
     uint32_t best_i = 0xffffffffu;
@@ -170,13 +200,31 @@ __global__ __launch_bounds__(256) void select_embed_kernel(const GemvArgs a) {
     }
 }
 
+// The row a lane finishes (lanes 16..63 repeat rows 0..15), clamped to the
+// matrix, and what its epilogue needs: the row's scale (row-scale mode) and
+// the epilogue's other inputs.
+struct TileIn {
+    int64_t row_scale;
+    EpiIn epi;
+};
+
 template <int MODE>
-__device__ void finish_tile(const GemvArgs& a, uint32_t tile, uint32_t token, dn::i128 t, uint32_t lane) {
+__device__ __forceinline__ TileIn tile_inputs(const GemvArgs& a, uint32_t tile, uint32_t token, uint32_t lane) {
+    const uint32_t row = min(tile * Q8_TILE_ROWS + (lane & (Q8_TILE_ROWS - 1)), a.w.rows - 1);
+    TileIn in;
+    in.row_scale = MODE == Q8_SCALE_ROW ? a.w.row_scale[row] : 0;
+    in.epi = epilogue_inputs(a, row, token);
+    return in;
+}
+
+template <int MODE>
+__device__ __forceinline__ void finish_tile(const GemvArgs& a, uint32_t tile, uint32_t token, dn::i128 t, uint32_t lane,
+                            const TileIn& in) {
     const Q8View& w = a.w;
     const uint32_t row = tile * Q8_TILE_ROWS + lane;
     int32_t v = 0;
     if (lane < Q8_TILE_ROWS) {
-        if (MODE == Q8_SCALE_ROW && row < w.rows) t = t * (dn::i128)w.row_scale[row];
+        if (MODE == Q8_SCALE_ROW) t = t * (dn::i128)in.row_scale;
         v = dn::round_to_i32(t, 24);
     }
     const int32_t partner = __shfl_xor(v, 1);  // the other row of an even/odd pair
@@ -185,7 +233,7 @@ __device__ void finish_tile(const GemvArgs& a, uint32_t tile, uint32_t token, dn
         return;
     }
     if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
-    store_output(a, row, token, v, partner);
+    store_output_in(a, row, token, v, partner, in.epi);
 }
 
 // Stages x[4*i0 .. 4*i1) (after the optional rms_norm: mul_sat(mul_sat(v,
@@ -246,15 +294,24 @@ __device__ __forceinline__ int64_t sumsq4(int64_t s, int4 v) {
 
 constexpr uint32_t XROUND = 4;  // int4 loads a thread has in flight per staging round
 
+// Barrier for LDS traffic only: global loads still in flight (the weight
+// prefetch) stay in flight, where __syncthreads would wait for them.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // The persistent kernel's prologue: the row's rms_norm scale when asked
 // (sum of squares: saturating, non-negative terms, so order-free) and every
 // digit plane of the row in LDS. A thread issues XROUND 16-byte loads (with
 // their norm weights) before it uses any of them; a row of at most
 // XROUND * GEMV_THREADS dwords is read once and kept in registers between
-// the two steps. Returns the digits the row needs.
-template <int NT>
-__device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes, int64_t* ssq,
-                         int32_t* s_scale, uint32_t tid) {
+// the two steps. issue() runs once, right after the first round's loads are
+// issued: the weight loads it issues queue behind the row's, and only LDS
+// barriers follow, so they stay in flight through the staging. Returns the
+// digits the row needs.
+template <int NT, typename Issue>
+__device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes, int64_t* ssq,
+                         uint32_t tid, Issue&& issue) {
     const uint32_t lane = tid & 63, wave = tid >> 6;
     const bool norm = a.prologue == PRO_RMSNORM;
     const int4* x4 = (const int4*)x;
@@ -262,7 +319,8 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
     // load is unconditional and issued in program order.
     const int4* n4 = norm ? (const int4*)a.norm_w : x4;
     // Out-of-range slots load the row's last dword (always valid) and are
-    // dropped afterwards, so no load waits on a branch.
+    // dropped afterwards: no load sits behind a branch, so the counted waits
+    // for them stay exact and the weight loads issued next stay in flight.
     auto load_round = [&](uint32_t i0, int4 (&v)[XROUND], int4 (&nw)[XROUND]) {
 #pragma unroll
         for (uint32_t u = 0; u < XROUND; u++) v[u] = x4[min(i0 + u * NT + tid, pw - 1)];
@@ -287,29 +345,30 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
         }
         return need;
     };
+    // Every wave forms the sum of the wave totals itself: one barrier.
     auto finish_scale = [&](int64_t s) -> int32_t {
         s = wave_sum_sat_nonneg(s);
         if (lane == 0) ssq[wave] = s;
-        __syncthreads();
-        if (tid == 0) {
-            int64_t t = 0;
-            for (int i = 0; i < NT / 64; i++) t = dn::acc_add_sat(t, ssq[i]);
-            *s_scale = dn::rms_scale_from_sum(t, pw * 4, a.norm_eps);
-        }
-        __syncthreads();
-        return *s_scale;
+        lds_barrier();
+        int64_t t = 0;
+        for (int i = 0; i < NT / 64; i++) t = dn::acc_add_sat(t, ssq[i]);
+        return dn::rms_scale_from_sum(t, pw * 4, a.norm_eps);
     };
     int4 v[XROUND], nw[XROUND];
     if (pw <= XROUND * NT) {
         load_round(0, v, nw);
+        issue();
         const int32_t scale = norm ? finish_scale(round_sumsq(0, v, 0)) : 0;
         return round_stage(0, v, nw, scale, 1);
     }
     int32_t scale = 0;
+    bool issued = false;
     if (norm) {
         int64_t s = 0;
         for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * NT) {
             load_round(i0, v, nw);
+            if (!issued) issue();
+            issued = true;
             s = round_sumsq(i0, v, s);
         }
         scale = finish_scale(s);
@@ -317,52 +376,20 @@ __device__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint3
     int need = 1;
     for (uint32_t i0 = 0; i0 < pw; i0 += XROUND * NT) {
         load_round(i0, v, nw);
+        if (!issued) issue();
+        issued = true;
         need = round_stage(i0, v, nw, scale, need);
     }
     return need;
 }
 
-// One block's contribution to the lane's accumulator.
-template <int L, int MODE>
-__device__ __forceinline__ void accumulate_block(const uint4 q0, const uint4 q1, uint32_t sbits, int64_t sc64,
-                                                 const uint32_t* lb, uint32_t pw, int64_t& acc64, dn::i128& acc128) {
-    const int64_t bs = block_sum_pw<L>(q0, q1, lb, pw);
-    if constexpr (MODE == Q8_SCALE_ROW) {
-        acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
-    } else if constexpr (MODE == Q8_SCALE_F16) {
-        const uint32_t e = (sbits >> 10) & 0x1f;
-        const int64_t m = (int64_t)(sbits & 0x3ff) | (e ? 1024 : 0);
-        int64_t p = bs * m;  // < 2^55
-        if (sbits & 0x8000) p = -p;
-        acc128 += (dn::i128)p << (e ? e - 1 : 0);
-    } else {
-        acc128 += (dn::i128)bs * (dn::i128)sc64;
-    }
-}
-
-// accumulate_block with the digit count L a runtime value (uniform over the
-// workgroup, so the plane loop's branches are scalar).
+// One block's contribution to the lane's accumulator (L digit planes,
+// uniform over the wave).
 template <int MODE>
-__device__ __forceinline__ void accumulate_block_rt(const uint4 q0, const uint4 q1, uint32_t sbits, int64_t sc64,
-                                                    const uint32_t* lb, uint32_t pw, int L, int64_t& acc64,
-                                                    dn::i128& acc128) {
-    int64_t bs = 0;
-#pragma unroll
-    for (int l = 0; l < MAX_LIMBS; l++) {
-        if (l < L) {
-            const uint32_t* p = lb + l * pw;
-            int s = 0;
-            s = __builtin_amdgcn_sdot4((int)q0.x, (int)p[0], s, false);
-            s = __builtin_amdgcn_sdot4((int)q0.y, (int)p[1], s, false);
-            s = __builtin_amdgcn_sdot4((int)q0.z, (int)p[2], s, false);
-            s = __builtin_amdgcn_sdot4((int)q0.w, (int)p[3], s, false);
-            s = __builtin_amdgcn_sdot4((int)q1.x, (int)p[4], s, false);
-            s = __builtin_amdgcn_sdot4((int)q1.y, (int)p[5], s, false);
-            s = __builtin_amdgcn_sdot4((int)q1.z, (int)p[6], s, false);
-            s = __builtin_amdgcn_sdot4((int)q1.w, (int)p[7], s, false);
-            bs += (int64_t)s << (8 * l);
-        }
-    }
+__device__ __forceinline__ void accumulate_block(const uint4 q0, const uint4 q1, uint32_t sbits, int64_t sc64,
+                                                 const uint32_t* lb, uint32_t pw, int L, int64_t& acc64,
+                                                 dn::i128& acc128) {
+    const int64_t bs = block_sum_planes(q0, q1, lb, pw, L);
     if constexpr (MODE == Q8_SCALE_ROW) {
         acc64 += bs;  // |bs| < 2^44 and at most 2^17 blocks: no overflow
     } else if constexpr (MODE == Q8_SCALE_F16) {
@@ -407,36 +434,55 @@ __device__ __forceinline__ uint32_t lane_block_count(uint32_t nb, uint32_t slot,
     return slot < nb ? (nb - slot + nslots - 1) / nslots : 0;
 }
 
+// One batch's blocks (k0, k0 + 1, ... of the lane's) into the accumulator.
+// Slots past the lane's last block were fetched as that block again; their
+// planes are read at the same clamped index and their sums dropped, so no
+// read waits on a branch.
+template <int MODE>
+__device__ __forceinline__ void consume_batch(const BlockBatch& bb, uint32_t k0, uint32_t cnt, uint32_t slot,
+                                              uint32_t nslots, uint32_t last, const uint32_t* planes, uint32_t pw,
+                                              int L, int64_t& acc64, dn::i128& acc128) {
+#pragma unroll
+    for (int u = 0; u < BATCH; u++) {
+        const uint32_t b = min(slot + (k0 + u) * nslots, last);
+        int64_t a64 = 0;
+        dn::i128 a128 = 0;
+        accumulate_block<MODE>(bb.q[u][0], bb.q[u][1], bb.s[u], bb.w[u], planes + b * 8, pw, L, a64, a128);
+        if (k0 + u < cnt) {
+            acc64 += a64;
+            acc128 += a128;
+        }
+    }
+}
+
 // All of one tile's blocks this lane owns (slot, slot + nslots, ...), against
-// L digit planes covering the whole row (plane stride pw dwords). Loads run
-// one batch ahead of the arithmetic; the first batch is fetched here unless
-// the caller has already issued it into `cur`.
+// L digit planes covering the whole row (plane stride pw dwords). Two
+// batches are in flight while one is summed; the first two are fetched here
+// unless the caller has already issued them into b0 and b1.
 template <int MODE>
 __device__ __forceinline__ void tile_blocks(const Q8View& w, uint32_t tile, uint32_t slot, uint32_t nslots, uint32_t r,
                                             const uint32_t* planes, uint32_t pw, int L, int64_t& acc64,
-                                            dn::i128& acc128, BlockBatch& cur, bool prefetched) {
+                                            dn::i128& acc128, BlockBatch& b0, BlockBatch& b1, bool prefetched) {
     const uint32_t cnt = lane_block_count(w.nb, slot, nslots);
     if (cnt == 0) return;
     const uint32_t last = slot + (cnt - 1) * nslots;
-    if (!prefetched) fetch_batch<MODE>(w, tile, slot, nslots, last, r, 0, cur);
-    BlockBatch nxt;
-    for (uint32_t k0 = 0; k0 < cnt; k0 += BATCH) {
-        if (k0 + BATCH < cnt) fetch_batch<MODE>(w, tile, slot, nslots, last, r, k0 + BATCH, nxt);
-#pragma unroll
-        for (int u = 0; u < BATCH; u++) {
-            if (k0 + u < cnt) {
-                const uint32_t b = slot + (k0 + u) * nslots;
-                accumulate_block_rt<MODE>(cur.q[u][0], cur.q[u][1], cur.s[u], cur.w[u], planes + b * 8, pw, L, acc64,
-                                          acc128);
-            }
+    if (!prefetched) {
+        fetch_batch<MODE>(w, tile, slot, nslots, last, r, 0, b0);
+        fetch_batch<MODE>(w, tile, slot, nslots, last, r, BATCH, b1);
+    }
+    for (uint32_t k0 = 0; k0 < cnt; k0 += 2 * BATCH) {
+        consume_batch<MODE>(b0, k0, cnt, slot, nslots, last, planes, pw, L, acc64, acc128);
+        if (k0 + 2 * BATCH < cnt) fetch_batch<MODE>(w, tile, slot, nslots, last, r, k0 + 2 * BATCH, b0);
+        if (k0 + BATCH < cnt) {
+            consume_batch<MODE>(b1, k0 + BATCH, cnt, slot, nslots, last, planes, pw, L, acc64, acc128);
+            if (k0 + 3 * BATCH < cnt) fetch_batch<MODE>(w, tile, slot, nslots, last, r, k0 + 3 * BATCH, b1);
         }
-        cur = nxt;
     }
 }
 
 template <int MODE>
 __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a) {
-    __shared__ uint32_t lds[MAX_LIMBS * KC_WORDS];
+    __shared__ __align__(16) uint32_t lds[MAX_LIMBS * KC_WORDS];
     __shared__ dn::i128 red[GEMV_WAVES][Q8_TILE_ROWS];
     __shared__ int64_t ssq[GEMV_WAVES];
     __shared__ int32_t s_scale;
@@ -518,7 +564,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
     if (lane < Q8_TILE_ROWS)
 #pragma unroll
         for (int i = 0; i < GEMV_WAVES; i++) t += red[i][lane];
-    finish_tile<MODE>(a, tile, token, t, lane);
+    finish_tile<MODE>(a, tile, token, t, lane, tile_inputs<MODE>(a, tile, token, lane));
 }
 
 // W waves per workgroup: 8 (two workgroups per CU) for matrices with many
@@ -526,11 +572,11 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
 // tile per CU, so that its few tiles still keep every wave slot busy.
 template <int MODE, int W>
 __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split) {
-    extern __shared__ uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
+    extern __shared__ __align__(16) uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
     __shared__ dn::i128 red[W][Q8_TILE_ROWS];
+    __shared__ TileIn s_in[W * Q8_TILE_ROWS];  // the first group's epilogue inputs, by tile and row
     __shared__ int64_t ssq[W];
-    __shared__ int32_t s_scale;
-    __shared__ int s_limbs;
+    __shared__ int s_need[W];
 
     const uint32_t tid = threadIdx.x;
     const uint32_t wave = tid >> 6, lane = tid & 63;
@@ -546,50 +592,81 @@ __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a
     const uint32_t part = wave % split;
     const uint32_t slot = part * 4 + g, nslots = split * 4;
 
-    // The first batch of this wave's first tile goes out before the row is
-    // staged (the weights do not depend on it), so the two latencies overlap.
-    BlockBatch cur;
-    bool prefetched = false;
-    {
-        const uint32_t tile0 = blockIdx.x * per_group + wave / split;
+    // The first two batches of this wave's first tile go out right after the
+    // row's own loads (the weights do not depend on the row), so the weight
+    // latency runs under the staging.
+    // Unconditional, from clamped indices (a wave past the last tile or a
+    // lane without blocks reads valid blocks it never uses): a load behind a
+    // branch would make the counted waits of the staging wait for it.
+    //
+    // A barrier first lets every wave's row loads reach the memory pipeline
+    // ahead of any wave's weight loads. Behind the weights, the first
+    // group's epilogue inputs (row scales, residuals, rotations): one entry
+    // per thread (clamped likewise), waited for only when the sums are done
+    // and parked in LDS for the lanes that finish each row.
+    BlockBatch b0, b1;
+    const uint32_t nin = per_group * Q8_TILE_ROWS;
+    TileIn in_mine;
+    auto issue = [&]() __attribute__((always_inline)) {
+        __builtin_amdgcn_s_barrier();
+        const uint32_t tile0 = min(blockIdx.x * per_group + wave / split, w.tiles - 1);
         const uint32_t cnt = lane_block_count(w.nb, slot, nslots);
-        if (blockIdx.x < groups && tile0 < w.tiles && cnt != 0) {
-            fetch_batch<MODE>(w, tile0, slot, nslots, slot + (cnt - 1) * nslots, r, 0, cur);
-            prefetched = true;
-        }
-    }
+        const uint32_t last = cnt ? slot + (cnt - 1) * nslots : w.nb - 1;
+        fetch_batch<MODE>(w, tile0, slot, nslots, last, r, 0, b0);
+        fetch_batch<MODE>(w, tile0, slot, nslots, last, r, BATCH, b1);
+        in_mine = tile_inputs<MODE>(a, min(blockIdx.x * per_group + (tid % nin) / Q8_TILE_ROWS, w.tiles - 1), token,
+                                    tid % nin);
+    };
 
     // Once per workgroup: the norm scale and every digit plane of the row.
-    if (tid == 0) s_limbs = 1;
-    __syncthreads();
-    const int need = stage_row<W * 64>(a, x, pw, planes, ssq, &s_scale, tid);
-    const int wave_need = wave_max_int(need);  // one LDS atomic per wave, not per lane
-    if (lane == 0) atomicMax(&s_limbs, wave_need);
-    __syncthreads();
-    const int limbs = s_limbs;
+    const int need = stage_row<W * 64>(a, x, pw, planes, ssq, tid, issue);
+    const int wave_need = wave_max_int(need);
+    if (lane == 0) s_need[wave] = wave_need;
+    lds_barrier();
+    int limbs = s_need[0];
+#pragma unroll
+    for (int i = 1; i < W; i++) limbs = max(limbs, s_need[i]);
 
-    for (uint32_t grp = blockIdx.x; grp < groups; grp += gridDim.x) {
+    // One group of tiles; the first group is the workgroup's own (its
+    // weights and epilogue inputs already issued), further ones (more groups
+    // than workgroups) come after it.
+    const int L = __builtin_amdgcn_readfirstlane(limbs);
+    auto group = [&](uint32_t grp, bool first) __attribute__((always_inline)) {
         const uint32_t tile = grp * per_group + wave / split;
         int64_t acc64 = 0;
         dn::i128 acc128 = 0;
-        if (tile < w.tiles) tile_blocks<MODE>(w, tile, slot, nslots, r, planes, pw, limbs, acc64, acc128, cur, prefetched);
-        prefetched = false;
+        if (tile < w.tiles) tile_blocks<MODE>(w, tile, slot, nslots, r, planes, pw, L, acc64, acc128, b0, b1, first);
         dn::i128 total = MODE == Q8_SCALE_ROW ? (dn::i128)acc64 : acc128;
         total = kgroup_sum(total);
+        if (first) {
+            if (tid < nin) s_in[tid] = in_mine;
+            __syncthreads();
+        }
         if (split == 1) {
-            if (tile < w.tiles) finish_tile<MODE>(a, tile, token, total, lane);
-            continue;
+            if (tile < w.tiles)
+                finish_tile<MODE>(a, tile, token, total, lane,
+                                  first ? s_in[(wave / split) * Q8_TILE_ROWS + r] : tile_inputs<MODE>(a, tile, token, lane));
+            return;
         }
         if (g == 0) red[wave][r] = total;
         __syncthreads();
         if (part == 0 && tile < w.tiles) {
+            // Every partial of the workgroup is read (all loads in flight
+            // together); those of the tile's split waves are summed.
             dn::i128 t = 0;
-            if (lane < Q8_TILE_ROWS)
-                for (uint32_t i = 0; i < split; i++) t += red[wave + i][lane];
-            finish_tile<MODE>(a, tile, token, t, lane);
+#pragma unroll
+            for (uint32_t i = 0; i < W; i++) {
+                const dn::i128 e = red[(wave + i) % W][r];
+                if (i < split) t += e;
+            }
+            finish_tile<MODE>(a, tile, token, t, lane,
+                              first ? s_in[(wave / split) * Q8_TILE_ROWS + r] : tile_inputs<MODE>(a, tile, token, lane));
         }
         __syncthreads();
-    }
+    };
+    group(blockIdx.x, true);
+#pragma unroll 1
+    for (uint32_t grp = blockIdx.x + gridDim.x; grp < groups; grp += gridDim.x) group(grp, false);
 }
 
 // One thread per (row, block): copies the 32 weights into the tile layout

@@ -434,7 +434,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.q_rows = qw;
         g.kv_rows = kvw;
         g.k_cache = s->k_cache[l];
-        g.k_pos_stride = s->max_positions;
+        g.k_pos_stride = s->k_pos_stride;
         g.v_cache = s->v_cache[l];
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
@@ -443,7 +443,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         a.q = s->q;
         a.q_stride = qw;
         a.k_cache = s->k_cache[l];
-        a.k_pos_stride = s->max_positions;
+        a.k_pos_stride = s->k_pos_stride;
         a.v_cache = s->v_cache[l];
         a.kv_stride = kvw;
         a.ctx = s->ctx;
@@ -572,7 +572,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         qa.q_out = s->q;
         qa.q_stride = qw;
         qa.k_cache = s->k_cache[l];
-        qa.k_pos_stride = s->max_positions;
+        qa.k_pos_stride = s->k_pos_stride;
         qa.v_cache = s->v_cache[l];
         RT_CHECK(iris_gemma_qkv_finish_launch(qa, rows, st));
         // 3. attention over the window of the source layer's cache (:692-845)
@@ -580,7 +580,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         a.q = s->q;
         a.q_stride = qw;
         a.k_cache = s->k_cache[L.kv_source];
-        a.k_pos_stride = s->max_positions;
+        a.k_pos_stride = s->k_pos_stride;
         a.v_cache = s->v_cache[L.kv_source];
         a.kv_stride = kvw;
         a.ctx = s->ctx;
@@ -756,6 +756,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     if (!s) return IRIS_E_NOMEM;
     s->model = m;
     s->max_positions = max_positions;
+    s->k_pos_stride = (max_positions + 63) & ~63u;
     s->max_rows = max_rows;
     const size_t qw = (size_t)d.heads * m->max_head_dim;
     hipError_t st = hipStreamCreate(&s->stream);
@@ -763,7 +764,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     s->v_cache.assign(d.layers, nullptr);
     for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++) {
         const size_t kvw = m->layers[l].kv_rows;
-        st = hipMalloc((void**)&s->k_cache[l], (size_t)max_positions * kvw * 4);
+        st = hipMalloc((void**)&s->k_cache[l], (size_t)s->k_pos_stride * kvw * 4);
         if (st == hipSuccess) st = hipMalloc((void**)&s->v_cache[l], (size_t)max_positions * kvw * 4);
     }
     auto alloc = [&](int32_t** p, size_t n) {

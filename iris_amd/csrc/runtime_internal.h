@@ -64,6 +64,7 @@ struct IrisModel {
 struct IrisSession {
     IrisModel* model = nullptr;
     uint32_t max_positions = 0, max_rows = 0;
+    uint32_t k_pos_stride = 0;  // positions per row of the transposed K cache: max_positions rounded up to 64
     hipStream_t stream = nullptr;
     std::vector<int32_t*> k_cache, v_cache;  // per layer [position][kv_heads*head_dim]
     int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;

@@ -128,3 +128,29 @@ def test_silu_against_oracle():
     got = dout.to_array(np.int32, (x.size,))
     want = np.array([O.dn_silu(int(v)) for v in x], np.int32)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("family", ["mistral", "gemma"])
+def test_long_context_decode_matches_oracle(family):
+    # One-row decode attention past several rounds of its key loop (512
+    # positions per round at head size 128, 1024 at 64), with a sliding
+    # window whose first visible position moves through every offset in a
+    # group of four; every logit compared with the oracle.
+    prompt_len, tokens, max_pos = 1030, 6, 1100
+    if family == "mistral":
+        m = synth.mistral_model(256, 2, 8, 2, 128, 512, 512, seed=41)
+    else:
+        shape = synth.gemma_shape(256, 2, 4, 1, 64, 512, 64, sliding_window=701,
+                                  layer_types=["sliding_attention", "full_attention"])
+        m = synth.gemma_model(shape, 512, seed=43)
+    prompt = synth.token_ids(13, prompt_len, m.vocab)
+    print(f"long-context decode, {family}", flush=True)
+    dm = DeviceModel(m)
+    s = Session(dm, max_pos, prompt_len)
+    got = s.generate(prompt, tokens, keep_logits=True)
+    r = cpu.OracleRun(m, max_pos)
+    want_tokens, want_logits = r.generate(list(prompt), tokens, keep_logits=True)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+    s.free()
+    dm.free()
