@@ -733,18 +733,34 @@ void gemv_prepare_once() {
     if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
 }
 
-// Waves sharing one tile (of a workgroup's W): the fewest that give one
-// round of tile groups covering at least 7/8 of the resident workgroups
-// (wgs). Measured: a second, mostly empty round costs more than leaving an
-// eighth of the slots idle (N=14336, K=4096: split 4 at 448 of 512 groups
-// is 10% faster than split 8 at 1.75 rounds).
+// Waves sharing one tile (of a workgroup's W): the most that still give a
+// single round of tile groups (at most wgs), so every tile's blocks are
+// spread as thin as one round allows; when even two waves per tile need
+// more than one round, the fewest that cover 7/8 of the workgroups.
+// Measured: a second, mostly empty round costs more than leaving slots
+// idle (N=14336, K=4096: split 4 at 448 of 512 groups is 10% faster than
+// split 8 at 1.75 rounds); one wave per tile is slower at every size.
 uint32_t choose_split(uint32_t tiles, uint32_t w, uint64_t wgs) {
     if (g_split_override == 1 || g_split_override == 2 || g_split_override == 4 || g_split_override == 8 ||
         (g_split_override == 16 && w == 16))
         return g_split_override;
-    for (uint32_t s = 2; s < w; s *= 2)  // one wave per tile measured slower at every size
+    uint32_t best = 0;
+    for (uint32_t s = 2; s <= w; s *= 2)
+        if ((uint64_t)tiles * s / w <= wgs) best = s;
+    if (best) return best;
+    for (uint32_t s = 2; s < w; s *= 2)
         if ((uint64_t)tiles * s / w >= wgs * 7 / 8) return s;
     return w;
+}
+
+// Resident 8-wave workgroups to aim for: two per CU when each CU's share of
+// the matrix is large (the weight stream sets the time), one when it is
+// small: a second workgroup on a CU gets its row only behind the first
+// one's weight loads, and with little streaming to hide that it sets the
+// kernel's end (N=6144, K=4096: 192 workgroups 17% faster than 384).
+uint64_t gemv_workgroups(const Q8View& w) {
+    const uint64_t share = (uint64_t)w.rows * w.cols / (uint64_t)g_num_cus;
+    return share <= (128u << 10) ? (uint64_t)g_num_cus : (uint64_t)WGS_PER_CU * g_num_cus;
 }
 
 template <int W>
@@ -788,7 +804,7 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
         // 16-wave workgroup per CU (measured faster there; slower for short rows).
         if (a.w.tiles <= (uint32_t)g_num_cus && a.w.cols >= 8192)
             return launch_persistent<16>(a, stream, (uint64_t)g_num_cus);
-        return launch_persistent<8>(a, stream, (uint64_t)WGS_PER_CU * g_num_cus);
+        return launch_persistent<8>(a, stream, gemv_workgroups(a.w));
     }
     dim3 grid(a.w.tiles, a.tokens);
     switch (a.w.scale_mode) {
