@@ -32,10 +32,38 @@ __device__ __forceinline__ int limbs_needed(uint64_t d) {
     return (d >> 32) ? 5 : (d >> 24) ? 4 : (d >> 16) ? 3 : (d >> 8) ? 2 : 1;
 }
 
-__device__ __forceinline__ int64_t wave_sum_sat_nonneg(int64_t v) {
-    // Saturating sum of non-negative terms: min(true sum, i64::MAX) in any order.
-    for (int off = 32; off >= 1; off >>= 1) v = dn::acc_add_sat(v, __shfl_xor(v, off));
+// A 64-bit value from another lane of the same 16-lane row (DPP control
+// CTRL: a register move, no LDS round trip).
+template <int CTRL>
+__device__ __forceinline__ int64_t dpp64(int64_t v) {
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)((uint64_t)v >> 32), CTRL, 0xF, 0xF, false);
+    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
+}
+
+// Saturating sum of non-negative terms over each 16-lane row, in every lane
+// of the row: min(true sum, i64::MAX), the same in any order. Lanes swap
+// within quads (1, then 2 apart), then mirror within half rows and rows.
+// Every lane of the wave must be active.
+__device__ __forceinline__ int64_t row16_sum_sat_nonneg(int64_t v) {
+    v = dn::acc_add_sat(v, dpp64<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = dn::acc_add_sat(v, dpp64<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = dn::acc_add_sat(v, dpp64<0x141>(v));  // row_half_mirror
+    v = dn::acc_add_sat(v, dpp64<0x140>(v));  // row_mirror
     return v;
+}
+
+// The same over the whole wave: the four row sums through scalar registers.
+__device__ __forceinline__ int64_t wave_sum_sat_nonneg(int64_t v) {
+    v = row16_sum_sat_nonneg(v);
+    int64_t t = 0;
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
+        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), 16 * r);
+        t = dn::acc_add_sat(t, (int64_t)(((uint64_t)hi << 32) | lo));
+    }
+    return t;
 }
 
 __device__ __forceinline__ int wave_max_int(int v) {
@@ -232,6 +260,14 @@ __device__ __forceinline__ void finish_tile(const GemvArgs& a, uint32_t tile, ui
         head_select(a, v, row, lane, tile);
         return;
     }
+    if (a.ssq_out) {
+        // The tile's rows as stored (add_sat with the residual), squared and
+        // summed with saturation over the 16 lanes.
+        const bool own = lane < Q8_TILE_ROWS && row < w.rows;
+        const int32_t o = dn::add_sat(v, in.epi.res);
+        const int64_t sq = row16_sum_sat_nonneg(own ? (int64_t)o * o : 0);
+        if (lane == 0) a.ssq_out[tile] = sq;
+    }
     if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
     store_output_in(a, row, token, v, partner, in.epi);
 }
@@ -357,8 +393,27 @@ __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, ui
     int4 v[XROUND], nw[XROUND];
     if (pw <= XROUND * NT) {
         load_round(0, v, nw);
+        // The producer's per-tile sums of squares, when given: loaded with
+        // the row (unconditionally: the row itself stands in when unused),
+        // summed by every wave on its own, so no barrier waits for the
+        // slowest wave's row before the planes.
+        const bool slots = norm && a.ssq_in != nullptr;
+        constexpr uint32_t SPL = GEMV_SSQ_SLOTS / 64;
+        int64_t sl[SPL];
+#pragma unroll
+        for (uint32_t u = 0; u < SPL; u++)
+            sl[u] = slots ? a.ssq_in[min(lane + 64 * u, a.ssq_n - 1)] : ((const int64_t*)x)[u];
         issue();
-        const int32_t scale = norm ? finish_scale(round_sumsq(0, v, 0)) : 0;
+        int32_t scale = 0;
+        if (slots) {
+            int64_t t = 0;
+#pragma unroll
+            for (uint32_t u = 0; u < SPL; u++)
+                if (lane + 64 * u < a.ssq_n) t = dn::acc_add_sat(t, sl[u]);
+            scale = dn::rms_scale_from_sum(wave_sum_sat_nonneg(t), pw * 4, a.norm_eps);
+        } else if (norm) {
+            scale = finish_scale(round_sumsq(0, v, 0));
+        }
         return round_stage(0, v, nw, scale, 1);
     }
     int32_t scale = 0;
@@ -798,6 +853,9 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.w.cols % 32 || a.x_stride % 4 || ((uintptr_t)a.x & 15)) return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
     if (a.tokens > 65535) return IRIS_E_INVALID;
+    if ((a.ssq_out || a.ssq_in) && a.tokens != 1) return IRIS_E_INVALID;
+    if (a.ssq_out && a.epilogue != EPI_RESIDUAL) return IRIS_E_INVALID;
+    if (a.ssq_in && (a.prologue != PRO_RMSNORM || a.ssq_n == 0 || a.ssq_n > GEMV_SSQ_SLOTS)) return IRIS_E_INVALID;
     gemv_prepare_once();
     if (a.w.cols <= PERSISTENT_MAX_K) {
         // Long rows (K >= 8192) of a matrix with at most one tile per CU: one

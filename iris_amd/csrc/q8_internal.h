@@ -110,7 +110,18 @@ struct GemvArgs {
     // GEMM when this work space is given (null: the GEMV path).
     int8_t* planes;             // gemm_planes_bytes(cols, tokens): 5 digit planes, MFMA-operand tiled
     int32_t* token_limbs;       // [2][tokens]: digits each token's activations need, then its rms_norm scale
+    // One-token launches only. ssq_out (EPI_RESIDUAL): each tile's saturating
+    // sum of the squares of its outputs, slot [tile]. ssq_in (PRO_RMSNORM):
+    // such slots of the row being normed, ssq_n of them (at most
+    // GEMV_SSQ_SLOTS): the norm's sum of squares is their saturating sum
+    // (non-negative terms: the same in any grouping), so the workgroups skip
+    // their own reduction. Null: not used.
+    int64_t* ssq_out;
+    const int64_t* ssq_in;
+    uint32_t ssq_n;
 };
+
+constexpr uint32_t GEMV_SSQ_SLOTS = 256;
 
 // Bytes of the MFMA product's digit planes: 5 planes of the tokens rounded
 // up to whole 32-token tiles, times cols, 256-byte aligned.

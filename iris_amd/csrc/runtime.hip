@@ -413,6 +413,11 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     hipStream_t st = s->stream;
     // The rows' RoPE (sin, cos) pairs, shared by every layer.
     RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, st));
+    // One row: the residual products leave per-tile sums of squares for the
+    // norms after them (hidden rows in 16-row tiles, within the slot count).
+    const uint32_t h_tiles = (H + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
+    const bool slots = rows == 1 && h_tiles <= GEMV_SSQ_SLOTS;
+    s->ssq_x_valid = false;
     for (uint32_t l = 0; l < d.layers; l++) {
         const LayerWeights& L = m->layers[l];
         GemvArgs g{};
@@ -436,6 +441,10 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.k_cache = s->k_cache[l];
         g.k_pos_stride = s->k_pos_stride;
         g.v_cache = s->v_cache[l];
+        if (slots && l > 0) {
+            g.ssq_in = s->ssq_x;
+            g.ssq_n = h_tiles;
+        }
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 2. attention.
@@ -473,6 +482,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.out_stride = H;
         g.residual = s->x;
         g.residual_stride = H;
+        if (slots) g.ssq_out = s->ssq_att;
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 4. gated = mul(silu(W_gate m), W_up m), m = rms_norm(attended).
@@ -487,6 +497,10 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.epilogue = EPI_SWIGLU;
         g.out = s->gated;
         g.out_stride = d.ffn;
+        if (slots) {
+            g.ssq_in = s->ssq_att;
+            g.ssq_n = h_tiles;
+        }
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 5. x = W_down gated + attended.
@@ -500,10 +514,12 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.out_stride = H;
         g.residual = s->attended;
         g.residual_stride = H;
+        if (slots) g.ssq_out = s->ssq_x;
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         RT_CHECK(checkpoint_layer(s, sink, l, rows));
     }
+    s->ssq_x_valid = slots && d.layers > 0;
     return 0;
 }
 
@@ -668,6 +684,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
 }
 
 static int session_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+    s->ssq_x_valid = false;
     if (s->model->d.family == IRIS_FAMILY_GEMMA_DENSE) return gemma_pass(s, rows, sink);
     return mistral_pass(s, rows, sink);
 }
@@ -683,6 +700,10 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     g.prologue = PRO_RMSNORM;
     g.norm_w = m->final_norm;
     g.norm_eps = d.norm_eps;
+    if (rows == 1 && s->ssq_x_valid) {
+        g.ssq_in = s->ssq_x;
+        g.ssq_n = (d.hidden + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
+    }
     g.epilogue = EPI_HEAD_SELECT;
     g.softcap = m->head_softcap;
     g.out = s->logits;
@@ -774,6 +795,8 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
         st = hipMalloc((void**)&s->rope_sc, (size_t)max_rows * d.head_dim * sizeof(int64_t));
     alloc(&s->x, (size_t)max_rows * d.hidden);
     alloc(&s->attended, (size_t)max_rows * d.hidden);
+    if (st == hipSuccess) st = hipMalloc((void**)&s->ssq_x, GEMV_SSQ_SLOTS * sizeof(int64_t));
+    if (st == hipSuccess) st = hipMalloc((void**)&s->ssq_att, GEMV_SSQ_SLOTS * sizeof(int64_t));
     alloc(&s->q, (size_t)max_rows * qw);
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
@@ -834,6 +857,8 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->sel_partial);
     hipFree(s->planes);
     hipFree(s->token_limbs);
+    hipFree(s->ssq_x);
+    hipFree(s->ssq_att);
     hipFree(s->attn_scores);
     hipFree(s->attn_chunk_max);
     hipFree(s->attn_chunk_acc);

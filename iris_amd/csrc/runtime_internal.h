@@ -68,6 +68,10 @@ struct IrisSession {
     hipStream_t stream = nullptr;
     std::vector<int32_t*> k_cache, v_cache;  // per layer [position][kv_heads*head_dim]
     int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;
+    // One-row passes: per-tile sums of squares of x and attended, written by
+    // the residual products and read by the norms that follow them.
+    int64_t *ssq_x = nullptr, *ssq_att = nullptr;
+    bool ssq_x_valid = false;  // the last pass left ssq_x for the head's norm
     // gemma-dense only: raw q|k|v rows, a product's rows before their norm,
     // the PLE projections and inputs of every layer, the PLE gate output
     int32_t *qkv = nullptr, *tmp = nullptr, *ple_proj = nullptr, *ple_rows = nullptr, *ple_gated = nullptr;
