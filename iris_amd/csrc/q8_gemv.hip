@@ -345,15 +345,13 @@ __device__ __forceinline__ void lds_barrier() {
 // issued: the weight loads it issues queue behind the row's, and only LDS
 // barriers follow, so they stay in flight through the staging. Returns the
 // digits the row needs.
-template <int NT, typename Issue>
+template <int NT, bool NORM, typename Issue>
 __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes, int64_t* ssq,
                          uint32_t tid, Issue&& issue) {
     const uint32_t lane = tid & 63, wave = tid >> 6;
-    const bool norm = a.prologue == PRO_RMSNORM;
+    constexpr bool norm = NORM;
     const int4* x4 = (const int4*)x;
-    // Without a norm the weight loads read the row again (unused): every
-    // load is unconditional and issued in program order.
-    const int4* n4 = norm ? (const int4*)a.norm_w : x4;
+    const int4* n4 = (const int4*)a.norm_w;
     // Out-of-range slots load the row's last dword (always valid) and are
     // dropped afterwards: no load sits behind a branch, so the counted waits
     // for them stay exact and the weight loads issued next stay in flight.
@@ -361,7 +359,7 @@ __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, ui
 #pragma unroll
         for (uint32_t u = 0; u < XROUND; u++) v[u] = x4[min(i0 + u * NT + tid, pw - 1)];
 #pragma unroll
-        for (uint32_t u = 0; u < XROUND; u++) nw[u] = n4[min(i0 + u * NT + tid, pw - 1)];
+        for (uint32_t u = 0; u < XROUND; u++) nw[u] = NORM ? n4[min(i0 + u * NT + tid, pw - 1)] : make_int4(0, 0, 0, 0);
         __builtin_amdgcn_sched_barrier(0);
     };
     auto round_sumsq = [&](uint32_t i0, const int4 (&v)[XROUND], int64_t s) {
@@ -625,7 +623,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
 // W waves per workgroup: 8 (two workgroups per CU) for matrices with many
 // tiles, 16 (one per CU, the same 16 waves) when a matrix has at most one
 // tile per CU, so that its few tiles still keep every wave slot busy.
-template <int MODE, int W>
+template <int MODE, int W, bool NORM>
 __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split) {
     extern __shared__ __align__(16) uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
     __shared__ dn::i128 red[W][Q8_TILE_ROWS];
@@ -674,7 +672,7 @@ __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a
     };
 
     // Once per workgroup: the norm scale and every digit plane of the row.
-    const int need = stage_row<W * 64>(a, x, pw, planes, ssq, tid, issue);
+    const int need = stage_row<W * 64, NORM>(a, x, pw, planes, ssq, tid, issue);
     const int wave_need = wave_max_int(need);
     if (lane == 0) s_need[wave] = wave_need;
     lds_barrier();
@@ -781,9 +779,18 @@ void gemv_prepare_once() {
         g_num_cus = prop.multiProcessorCount;
     if (g_num_cus <= 0) g_num_cus = 256;
     const int bytes = MAX_LIMBS * PERSISTENT_MAX_K;
-    for (const void* f : {(const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 8>, (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 8>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 8>, (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 16>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 16>, (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 16>})
+    for (const void* f : {(const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 8, false>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 8, false>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 8, false>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 16, false>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 16, false>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 16, false>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 8, true>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 8, true>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 8, true>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 16, true>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 16, true>,
+                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 16, true>})
         hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
     if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
 }
@@ -825,10 +832,20 @@ int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) 
     const uint32_t wgs = min(groups, (uint32_t)resident);
     const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
     dim3 grid(wgs, a.tokens);
-    switch (a.w.scale_mode) {
-        case Q8_SCALE_ROW: hipLaunchKernelGGL((q8_gemv_persistent<Q8_SCALE_ROW, W>), grid, dim3(W * 64), shmem, stream, a, split); break;
-        case Q8_SCALE_F16: hipLaunchKernelGGL((q8_gemv_persistent<Q8_SCALE_F16, W>), grid, dim3(W * 64), shmem, stream, a, split); break;
-        default: hipLaunchKernelGGL((q8_gemv_persistent<Q8_SCALE_I64, W>), grid, dim3(W * 64), shmem, stream, a, split); break;
+    const bool norm = a.prologue == PRO_RMSNORM;
+    switch (a.w.scale_mode * 2 + (norm ? 1 : 0)) {
+#define IRIS_PERSISTENT(M, N)                                                                                   \
+    case M * 2 + N:                                                                                             \
+        hipLaunchKernelGGL((q8_gemv_persistent<M, W, N>), grid, dim3(W * 64), shmem, stream, a, split); \
+        break;
+        IRIS_PERSISTENT(Q8_SCALE_ROW, false)
+        IRIS_PERSISTENT(Q8_SCALE_ROW, true)
+        IRIS_PERSISTENT(Q8_SCALE_F16, false)
+        IRIS_PERSISTENT(Q8_SCALE_F16, true)
+        IRIS_PERSISTENT(Q8_SCALE_I64, false)
+        IRIS_PERSISTENT(Q8_SCALE_I64, true)
+#undef IRIS_PERSISTENT
+        default: return IRIS_E_INVALID;
     }
     return (int)hipGetLastError();
 }
