@@ -43,7 +43,7 @@ PEAK_HBM_GBPS = 8000.0
 # and WRITE_SIZE passes scaled by a 256 MiB device copy (fetch x2.000, write
 # x1.000): profiles/q8_gemv_row_scale_k4096_n14336.md. Re-measure when the
 # kernel or its layout changes.
-GEMV_TRAFFIC_BYTES = 59_314_000
+GEMV_TRAFFIC_BYTES = 59_357_000
 PROMPT = 512  # the prompt length of the timed workload
 DECODE_TOKENS = 512
 TEACHER_FORCED_ROWS = 2048
