@@ -46,21 +46,12 @@ struct AttnArgs {
     int scaled;              // 1: mistral scaled_score; 0: gemma requantized dot
     uint32_t scale_q32;
     uint32_t window;         // 0 = every earlier position is visible
-    // Scratch for the split decode path (one query row), sized for
-    // heads x ATTN_MAX_KEYS scores, heads x ATTN_MAX_CHUNKS chunk records.
-    int32_t* scores;         // [heads][ATTN_MAX_KEYS]
-    uint64_t* chunk_max;     // [heads][ATTN_MAX_CHUNKS]: (index << 32) | (uint32)score
-    int64_t* chunk_acc;      // [heads][ATTN_MAX_CHUNKS][head_dim]
-    int32_t* chunk_wsum;     // [heads][ATTN_MAX_CHUNKS]
-    int32_t* max_weight;     // [heads]: the first maximum's weight before the residual
     // Digit planes for the multi-row MFMA path (planes.q null: the scalar
     // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes /
     // attn_e_store_bytes.
     AttnPlanes planes;
 };
 
-constexpr uint32_t ATTN_CHUNK = 128;  // keys per workgroup in the split decode path
-constexpr uint32_t ATTN_MAX_CHUNKS = ATTN_MAX_KEYS / ATTN_CHUNK;
 
 // Attention for `tokens` query rows; max_keys bounds the visible keys of the
 // last row (checked against the kernel's capacity).

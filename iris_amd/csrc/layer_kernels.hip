@@ -12,232 +12,6 @@ __global__ __launch_bounds__(ATTN_MAX_THREADS) void attention_kernel(const AttnA
     attend_row(a, blockIdx.x, blockIdx.y, sm);
 }
 
-// ---- split decode attention: one query row, each head over key chunks ----
-//
-// Three launches per layer, each arranged so that its global loads are
-// issued together (one or two memory round trips per kernel) rather than
-// one after another: the kernels are latency-bound, not bandwidth-bound.
-// HD is the head size (32, 64, 128 or 256), so every loop unrolls.
-
-// Scores of one chunk of ATTN_CHUNK keys (512 threads: two groups of 64
-// keys, four dimension quarters each) and the chunk's first maximum. The
-// key loads are issued before the query is staged.
-template <uint32_t HD>
-__global__ __launch_bounds__(512) void attn_chunk_scores_kernel(const AttnArgs a) {
-    constexpr uint32_t QS = 4, DQ = HD / QS;
-    __shared__ int32_t s_q[HD];
-    __shared__ int64_t s_part[QS * ATTN_CHUNK];
-    __shared__ ArgMax s_am[8];
-    const uint32_t head = blockIdx.x, chunk = blockIdx.z;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kvh = head / (a.heads / a.kv_heads);
-    const uint32_t pos = (uint32_t)(*a.d_pos);
-    const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
-    const uint32_t n = pos - start + 1;
-    const uint32_t c0 = chunk * ATTN_CHUNK;
-    if (c0 >= n) return;
-    const uint32_t kg = wave / QS, qd = wave % QS;
-    const uint32_t key = c0 + kg * 64 + lane;
-    const bool live = key < n;
-    const int32_t* kk = a.k_cache + ((size_t)kvh * HD + (size_t)qd * DQ) * a.k_pos_stride + start + (live ? key : 0);
-    int32_t kv[DQ];
-#pragma unroll
-    for (uint32_t i = 0; i < DQ; i++) kv[i] = kk[(size_t)i * a.k_pos_stride];
-    for (uint32_t d = tid; d < HD; d += 512) s_q[d] = a.q[(size_t)head * HD + d];
-    __syncthreads();
-    uint64_t acc = 0;  // wrapping i64 (mac_bits, ops.rs:17-19)
-#pragma unroll
-    for (uint32_t i = 0; i < DQ; i++) acc += (uint64_t)((int64_t)s_q[qd * DQ + i] * kv[i]);
-    s_part[qd * ATTN_CHUNK + kg * 64 + lane] = live ? (int64_t)acc : 0;
-    __syncthreads();
-    ArgMax best{INT32_MIN, 0xffffffffu};
-    if (tid < ATTN_CHUNK && c0 + tid < n) {
-        uint64_t sum = 0;
-#pragma unroll
-        for (uint32_t i = 0; i < QS; i++) sum += (uint64_t)s_part[i * ATTN_CHUNK + tid];
-        const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)sum, a.scale_q32) : dn::requantize((int64_t)sum);
-        a.scores[(size_t)head * ATTN_MAX_KEYS + c0 + tid] = sc;
-        best = ArgMax{sc, c0 + tid};
-    }
-    best = wave_argmax(best);
-    if (lane == 0) s_am[wave] = best;
-    __syncthreads();
-    if (tid == 0) {
-        ArgMax m = s_am[0];
-        for (int i = 1; i < 8; i++) m = argmax_combine(m, s_am[i]);
-        a.chunk_max[(size_t)head * ATTN_MAX_CHUNKS + chunk] = ((uint64_t)m.i << 32) | (uint32_t)m.v;
-    }
-}
-
-// The softmax (ops.rs:233-261) as one chunk needs it, and the chunk's
-// weighted values. Every workgroup of a head recomputes the global first
-// maximum (from the chunk records) and every exp term (for their sum); it
-// then forms its own keys' weights, their saturating sum, and the wrapping
-// sums of w*v. The chunk's values are loaded first, while the softmax runs.
-template <uint32_t HD>
-__global__ __launch_bounds__(512) void attn_chunk_softmax_pv_kernel(const AttnArgs a) {
-    constexpr uint32_t NT = 512, NWV = NT / 64;
-    constexpr uint32_t DG = HD / 4;               // threads per key, 4 dimensions each
-    constexpr uint32_t GROUPS = NT / DG;          // keys in flight per round
-    constexpr uint32_t KPT = ATTN_CHUNK / GROUPS; // keys per thread
-    constexpr uint32_t SPT = ATTN_MAX_KEYS / NT;  // scores per thread, at most
-    __shared__ int64_t s_e[ATTN_CHUNK];
-    __shared__ int32_t s_w[ATTN_CHUNK];
-    __shared__ uint64_t s_rec[ATTN_MAX_CHUNKS];
-    __shared__ int64_t s_part[NT * 4];
-    __shared__ int64_t s_sum[NWV];
-    __shared__ int32_t s_wsum[NWV];
-    const uint32_t head = blockIdx.x, chunk = blockIdx.z;
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t kvh = head / (a.heads / a.kv_heads);
-    const uint32_t pos = (uint32_t)(*a.d_pos);
-    const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
-    const uint32_t n = pos - start + 1;
-    const uint32_t nchunks = (n + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    const uint32_t c0 = chunk * ATTN_CHUNK;
-    if (c0 >= n) return;
-    const uint32_t cn = min(ATTN_CHUNK, n - c0);
-
-    // 1. Issue every load: this chunk's values, the head's scores, the chunk records.
-    const uint32_t gi = tid / DG, d4 = (tid % DG) * 4;
-    const int32_t* vb = a.v_cache + (size_t)(start + c0) * a.kv_stride + (size_t)kvh * HD + d4;
-    int4 vv[KPT];
-#pragma unroll
-    for (uint32_t u = 0; u < KPT; u++) {
-        const uint32_t j = gi + u * GROUPS;
-        vv[u] = *(const int4*)(vb + (size_t)(j < cn ? j : 0) * a.kv_stride);
-    }
-    const int32_t* sc = a.scores + (size_t)head * ATTN_MAX_KEYS;
-    int32_t sv[SPT];
-#pragma unroll
-    for (uint32_t u = 0; u < SPT; u++) {
-        const uint32_t j = tid + u * NT;
-        sv[u] = j < n ? sc[j] : 0;
-    }
-    if (tid < nchunks) s_rec[tid] = a.chunk_max[(size_t)head * ATTN_MAX_CHUNKS + tid];
-    __syncthreads();
-
-    // 2. The first maximum over the chunk records (chunks in key order).
-    ArgMax m{INT32_MIN, 0xffffffffu};
-    for (uint32_t c = 0; c < nchunks; c++) {
-        const uint64_t r = s_rec[c];
-        m = argmax_combine(m, ArgMax{(int32_t)(uint32_t)r, (uint32_t)(r >> 32)});
-    }
-    // 3. sum_sat of every exp term (non-negative: order-free); keep this chunk's.
-    int64_t part = 0;
-#pragma unroll
-    for (uint32_t u = 0; u < SPT; u++) {
-        const uint32_t j = tid + u * NT;
-        if (j < n) {
-            const int64_t diff = (int64_t)m.v - sv[u];  // >= 0: m is the maximum
-            const int64_t e = (int64_t)dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
-            part = dn::acc_add_sat(part, e);
-            if (j >= c0 && j < c0 + cn) s_e[j - c0] = e;
-        }
-    }
-    part = wave_sum_sat64(part);
-    if (lane == 0) s_sum[wave] = part;
-    __syncthreads();
-    int64_t total = 0;
-    for (uint32_t i = 0; i < NWV; i++) total = dn::acc_add_sat(total, s_sum[i]);
-
-    // 4. This chunk's weights and their saturating sum.
-    int32_t wpart = 0;
-    if (tid < cn) {
-        const int32_t w = dn::softmax_weight_fast((uint64_t)s_e[tid], (uint64_t)total, 65536.0 / (double)total,
-                                                  4294967296.0 / (double)total);
-        s_w[tid] = w;
-        wpart = w;
-        if (c0 + tid == m.i) a.max_weight[head] = w;
-    }
-    wpart = wave_sum_sat32(wpart);
-    if (lane == 0) s_wsum[wave] = wpart;
-    __syncthreads();
-
-    // 5. Weighted values (wrapping i64) of the prefetched rows.
-    uint64_t acc[4] = {0, 0, 0, 0};
-#pragma unroll
-    for (uint32_t u = 0; u < KPT; u++) {
-        const uint32_t j = gi + u * GROUPS;
-        if (j < cn) {
-            const int64_t w = s_w[j];
-            acc[0] += (uint64_t)(w * vv[u].x);
-            acc[1] += (uint64_t)(w * vv[u].y);
-            acc[2] += (uint64_t)(w * vv[u].z);
-            acc[3] += (uint64_t)(w * vv[u].w);
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) s_part[tid * 4 + i] = (int64_t)acc[i];
-    __syncthreads();
-    for (uint32_t d = tid; d < HD; d += NT) {
-        const uint32_t t_dg = d / 4, t_i = d % 4;
-        uint64_t t = 0;
-#pragma unroll
-        for (uint32_t g = 0; g < GROUPS; g++) t += (uint64_t)s_part[(g * DG + t_dg) * 4 + t_i];
-        a.chunk_acc[((size_t)head * ATTN_MAX_CHUNKS + chunk) * HD + d] = (int64_t)t;
-    }
-    if (tid == 0) {
-        int32_t ws = 0;
-        for (uint32_t i = 0; i < NWV; i++) ws = dn::add_sat(ws, s_wsum[i]);
-        a.chunk_wsum[(size_t)head * ATTN_MAX_CHUNKS + chunk] = ws;
-    }
-}
-
-// Combines one head's chunk partials: the saturating sum of the chunk weight
-// sums, the residual on the first maximum as an exact correction term (its
-// weight changes from w to add_sat(w, ONE - sum)), and the rounding. The
-// records and partial sums are loaded together; only the first maximum's
-// value row waits for them.
-template <uint32_t HD>
-__global__ __launch_bounds__(256) void attn_chunk_combine_kernel(const AttnArgs a) {
-    __shared__ uint64_t s_rec[ATTN_MAX_CHUNKS];
-    __shared__ int32_t s_ws[ATTN_MAX_CHUNKS];
-    const uint32_t head = blockIdx.x, tid = threadIdx.x;
-    const uint32_t kvh = head / (a.heads / a.kv_heads);
-    const uint32_t pos = (uint32_t)(*a.d_pos);
-    const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
-    const uint32_t n = pos - start + 1;
-    const uint32_t nchunks = (n + ATTN_CHUNK - 1) / ATTN_CHUNK;
-    if (tid < nchunks) {
-        s_rec[tid] = a.chunk_max[(size_t)head * ATTN_MAX_CHUNKS + tid];
-        s_ws[tid] = a.chunk_wsum[(size_t)head * ATTN_MAX_CHUNKS + tid];
-    }
-    const int32_t wm = a.max_weight[head];
-    uint64_t t = 0;
-    if (tid < HD) {
-        const int64_t* ca = a.chunk_acc + (size_t)head * ATTN_MAX_CHUNKS * HD + tid;
-#pragma unroll
-        for (uint32_t c = 0; c < ATTN_MAX_CHUNKS; c++)
-            if (c < nchunks) t += (uint64_t)ca[(size_t)c * HD];
-    }
-    __syncthreads();
-    ArgMax m{INT32_MIN, 0xffffffffu};
-    int32_t ws = 0;
-    for (uint32_t c = 0; c < nchunks; c++) {
-        const uint64_t r = s_rec[c];
-        m = argmax_combine(m, ArgMax{(int32_t)(uint32_t)r, (uint32_t)(r >> 32)});
-        ws = dn::add_sat(ws, s_ws[c]);
-    }
-    if (tid < HD) {
-        const int64_t fix = (int64_t)dn::add_sat(wm, dn::sub_sat(dn::ONE_ACT, ws)) - wm;
-        t += (uint64_t)fix * (uint64_t)(int64_t)a.v_cache[(size_t)(start + m.i) * a.kv_stride + (size_t)kvh * HD + tid];
-        a.ctx[(size_t)head * HD + tid] = dn::requantize((int64_t)t);
-    }
-}
-
-template <uint32_t HD>
-int attention_split_launch(const AttnArgs& a, uint32_t chunks, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_chunk_scores_kernel<HD>, dim3(a.heads, 1, chunks), dim3(512), 0, stream, a);
-    hipError_t st = hipGetLastError();
-    if (st != hipSuccess) return (int)st;
-    hipLaunchKernelGGL(attn_chunk_softmax_pv_kernel<HD>, dim3(a.heads, 1, chunks), dim3(512), 0, stream, a);
-    st = hipGetLastError();
-    if (st != hipSuccess) return (int)st;
-    hipLaunchKernelGGL(attn_chunk_combine_kernel<HD>, dim3(a.heads), dim3(256), 0, stream, a);
-    return (int)hipGetLastError();
-}
-
 // One query row in one launch. Every workgroup of a head recomputes the
 // head's scores (the key loads of a round issued together), its first
 // maximum, exp terms and

@@ -464,11 +464,6 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         a.scaled = 1;
         a.scale_q32 = d.attention_scale_q32;
         a.window = 0;
-        a.scores = s->attn_scores;
-        a.chunk_max = s->attn_chunk_max;
-        a.chunk_acc = s->attn_chunk_acc;
-        a.chunk_wsum = s->attn_chunk_wsum;
-        a.max_weight = s->attn_max_weight;
         a.planes = s->attn_planes;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 3. attended = W_o ctx + x.
@@ -607,11 +602,6 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         a.head_dim = hd;
         a.scaled = 0;
         a.window = L.window;
-        a.scores = s->attn_scores;
-        a.chunk_max = s->attn_chunk_max;
-        a.chunk_acc = s->attn_chunk_acc;
-        a.chunk_wsum = s->attn_chunk_wsum;
-        a.max_weight = s->attn_max_weight;
         a.planes = s->attn_planes;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 4. attended = rms_norm(W_o ctx, post_attention) + x  (:879-892)
@@ -831,13 +821,6 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->d_pos, 1);
     alloc(&s->d_step, 1);
     if (st == hipSuccess) st = hipMalloc((void**)&s->sel_partial, (size_t)m->head->tiles * sizeof(uint64_t));
-    const size_t heads = d.heads;
-    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_scores, heads * ATTN_MAX_KEYS * sizeof(int32_t));
-    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_chunk_max, heads * ATTN_MAX_CHUNKS * sizeof(uint64_t));
-    if (st == hipSuccess)
-        st = hipMalloc((void**)&s->attn_chunk_acc, heads * ATTN_MAX_CHUNKS * m->max_head_dim * sizeof(int64_t));
-    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_chunk_wsum, heads * ATTN_MAX_CHUNKS * sizeof(int32_t));
-    if (st == hipSuccess) st = hipMalloc((void**)&s->attn_max_weight, heads * sizeof(int32_t));
     if (st != hipSuccess) {
         iris_session_free(s);
         return (int)st;
@@ -859,11 +842,6 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->token_limbs);
     hipFree(s->ssq_x);
     hipFree(s->ssq_att);
-    hipFree(s->attn_scores);
-    hipFree(s->attn_chunk_max);
-    hipFree(s->attn_chunk_acc);
-    hipFree(s->attn_chunk_wsum);
-    hipFree(s->attn_max_weight);
     hipFree(s->attn_planes.q);
     hipFree(s->attn_planes.k);
     hipFree(s->attn_planes.v);

@@ -85,11 +85,6 @@ struct IrisSession {
     bool keep_logits = false;
     uint64_t* sel_partial = nullptr;
     // split decode attention scratch
-    int32_t* attn_scores = nullptr;
-    uint64_t* attn_chunk_max = nullptr;
-    int64_t* attn_chunk_acc = nullptr;
-    int32_t* attn_chunk_wsum = nullptr;
-    int32_t* attn_max_weight = nullptr;
     int64_t* rope_sc = nullptr;      // mistral-dense: [max_rows][head_dim/2][sin, cos] of the pass's positions
     // multi-row attention digit planes (null for single-row sessions)
     AttnPlanes attn_planes{};
