@@ -189,16 +189,29 @@ __device__ __forceinline__ void head_select(const GemvArgs& a, int32_t v, uint32
 // Greedy selection (generation.rs:25-57) over the head's tile partials, in
 // tile (= token id) order with the first maximum kept, then the selected
 // token's embedding as the next pass's row (view_kernels.rs:37-57,
-// model.rs:316-330), and the step and position advanced.
-__global__ __launch_bounds__(256) void select_embed_kernel(const GemvArgs a) {
-    __shared__ int32_t s_v[4];
-    __shared__ uint32_t s_i[4];
+// model.rs:316-330), and the step and position advanced. With rope_next,
+// threads past the embedding's also form the next one-row pass's RoPE
+// (sin, cos) pairs (mistral.rs:84-109) at the advanced position, while the
+// partials are on their way.
+constexpr uint32_t SELECT_THREADS = 1024;
+
+__global__ __launch_bounds__(SELECT_THREADS) void select_embed_kernel(const GemvArgs a) {
+    __shared__ int32_t s_v[SELECT_THREADS / 64];
+    __shared__ uint32_t s_i[SELECT_THREADS / 64];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int32_t pos0 = *a.d_pos_rw;
     int32_t best = INT32_MIN;
     uint32_t best_i = 0xffffffffu;
-    for (uint32_t t = tid; t < a.w.tiles; t += 256) {
+    for (uint32_t t = tid; t < a.w.tiles; t += SELECT_THREADS) {
         const uint64_t p = a.sel_partial[t];
         argmax_combine(best, best_i, (int32_t)(uint32_t)p, (uint32_t)(p >> 32));
+    }
+    if (a.rope_next && tid >= SELECT_THREADS - a.rope_half) {
+        const uint32_t j = tid - (SELECT_THREADS - a.rope_half);
+        int64_t sn, cs;
+        dn::sin_cos_q30((int64_t)(uint32_t)(pos0 + (int32_t)a.rows_in_pass) * a.inv_freq[j], sn, cs);
+        a.rope_next[2 * j] = sn;
+        a.rope_next[2 * j + 1] = cs;
     }
     for (int off = 32; off >= 1; off >>= 1) argmax_combine(best, best_i, __shfl_xor(best, off), __shfl_xor(best_i, off));
     if (lane == 0) {
@@ -208,23 +221,22 @@ __global__ __launch_bounds__(256) void select_embed_kernel(const GemvArgs a) {
     __syncthreads();
     best = s_v[0];
     best_i = s_i[0];
-    for (int i = 1; i < 4; i++) argmax_combine(best, best_i, s_v[i], s_i[i]);
+    for (uint32_t i = 1; i < SELECT_THREADS / 64; i++) argmax_combine(best, best_i, s_v[i], s_i[i]);
     const uint32_t token = best_i;
     const uint8_t* er = a.embed_raw + (size_t)token * a.embed_row_bytes;
-    for (uint32_t c = tid; c < a.hidden; c += 256) {
+    for (uint32_t c = tid; c < a.hidden; c += SELECT_THREADS) {
         const uint8_t* blk = er + (size_t)(c / 32) * 34;
         const int64_t sc = dn::scale_q24((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
         int32_t e = dn::round_to_i32((dn::i128)((int64_t)(int8_t)blk[2 + c % 32] * sc), 8);
         if (a.embed_scale != 0) e = dn::mul_sat(e, a.embed_scale);
         a.x_next[c] = e;
     }
-    __syncthreads();
     if (tid == 0) {
         const int32_t step = *a.d_step;
         a.tokens_out[step] = (int32_t)token;
         if (a.ids_next) a.ids_next[0] = (int32_t)token;
         *a.d_step = step + 1;
-        *a.d_pos_rw = *a.d_pos_rw + (int32_t)a.rows_in_pass;
+        *a.d_pos_rw = pos0 + (int32_t)a.rows_in_pass;
     }
 }
 
@@ -860,7 +872,8 @@ int iris_device_cus() {
 }
 
 int iris_select_launch(const GemvArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(select_embed_kernel, dim3(1), dim3(256), 0, stream, a);
+    if (a.rope_next && (a.rope_half == 0 || a.rope_half > SELECT_THREADS / 2 || !a.inv_freq)) return IRIS_E_INVALID;
+    hipLaunchKernelGGL(select_embed_kernel, dim3(1), dim3(SELECT_THREADS), 0, stream, a);
     return (int)hipGetLastError();
 }
 

@@ -106,6 +106,8 @@ struct GemvArgs {
     int32_t* x_next;            // [hidden]
     int32_t* ids_next;          // nullable: the selected id is also stored here
     uint64_t* sel_partial;      // [tiles]: (index << 32) | (uint32)value of each tile's first maximum
+    int64_t* rope_next;         // nullable: the next one-row pass's RoPE (sin, cos) pairs, [rope_half][2]
+    uint32_t rope_half;         // pairs per position (head_dim / 2)
     // Multi-token products of row-scale matrices go through the int8 MFMA
     // GEMM when this work space is given (null: the GEMV path).
     int8_t* planes;             // gemm_planes_bytes(cols, tokens): 5 digit planes, MFMA-operand tiled

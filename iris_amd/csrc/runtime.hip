@@ -411,8 +411,11 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     const uint32_t H = d.hidden;
     const uint32_t qw = d.heads * d.head_dim, kvw = d.kv_heads * d.head_dim;
     hipStream_t st = s->stream;
-    // The rows' RoPE (sin, cos) pairs, shared by every layer.
-    RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, st));
+    // The rows' RoPE (sin, cos) pairs, shared by every layer (for a one-row
+    // pass after a selection, the selection kernel has formed them).
+    if (!(rows == 1 && s->rope_ready))
+        RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, st));
+    s->rope_ready = false;
     // One row: the residual products leave per-tile sums of squares for the
     // norms after them (hidden rows in 16-row tiles, within the slot count).
     const uint32_t h_tiles = (H + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
@@ -710,12 +713,21 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     g.x_next = s->x;
     g.ids_next = m->d.family == IRIS_FAMILY_GEMMA_DENSE ? s->ids : nullptr;
     g.sel_partial = s->sel_partial;
+    const bool rope = m->d.family != IRIS_FAMILY_GEMMA_DENSE;
+    if (rope) {
+        g.rope_next = s->rope_sc;
+        g.rope_half = d.head_dim / 2;
+        g.inv_freq = m->inv_freq;
+    }
     RT_CHECK(iris_gemv_launch(g, s->stream));
-    return iris_select_launch(g, s->stream);
+    RT_CHECK(iris_select_launch(g, s->stream));
+    s->rope_ready = rope;
+    return 0;
 }
 
 static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t count) {
     IrisModel* m = s->model;
+    s->rope_ready = false;
     for (uint32_t i = 0; i < count; i++)
         if (ids[i] < 0 || (uint32_t)ids[i] >= m->d.vocab) return IRIS_E_INVALID;
     RT_CHECK(hipMemsetAsync(s->d_pos, 0, sizeof(int32_t), s->stream));

@@ -72,6 +72,7 @@ struct IrisSession {
     // the residual products and read by the norms that follow them.
     int64_t *ssq_x = nullptr, *ssq_att = nullptr;
     bool ssq_x_valid = false;  // the last pass left ssq_x for the head's norm
+    bool rope_ready = false;   // the last selection left rope_sc for the next one-row pass
     // gemma-dense only: raw q|k|v rows, a product's rows before their norm,
     // the PLE projections and inputs of every layer, the PLE gate output
     int32_t *qkv = nullptr, *tmp = nullptr, *ple_proj = nullptr, *ple_rows = nullptr, *ple_gated = nullptr;
