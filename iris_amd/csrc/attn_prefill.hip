@@ -223,7 +223,8 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
     const bool qvalid = qrow < tokens;
     const uint32_t qpos = pos0 + qrow;
     const uint32_t qstart = (a.window == 0 || qpos + 1 <= a.window) ? 0 : qpos + 1 - a.window;
-    auto visible = [&](uint32_t key) { return qvalid && key >= qstart && key <= qpos; };
+    const uint32_t span = qpos - qstart;  // qstart <= key <= qpos, as one unsigned comparison
+    auto visible = [&](uint32_t key) { return qvalid & (key - qstart <= span); };
     v4i qf[LQK][DS];
     {
         const int8_t* qb = p.q + ((size_t)head * p.qt_cap + qt) * DS * FRAG + lane * 16;
@@ -250,10 +251,9 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t key = kt * 16 + 4 * grp + i;
-            if (visible(key) && sc[i] > best) {
-                best = sc[i];
-                best_key = key;
-            }
+            const bool take = visible(key) & (sc[i] > best);
+            best = take ? sc[i] : best;
+            best_key = take ? key : best_key;
         }
 #pragma unroll
         for (int l = 0; l < LQK; l++)
@@ -288,7 +288,7 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
             const uint32_t key = kt * 16 + 4 * grp + i;
             const int64_t diff = (int64_t)best - sc[i];
             uint64_t e = 0;
-            if (visible(key)) e = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
+            if (visible(key) & (diff < (1 << 20))) e = dn::softmax_exp_diff((uint32_t)diff);
             sum += e;
             ev[i] = e > 0xffffffffull ? 0xffffffffu : (uint32_t)e;
         }
@@ -333,22 +333,46 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
             const uint4 ec = en;
             if (kt + 1 < kt1) en = *(const uint4*)(estore + (size_t)(kt + 1) * 256);
             const uint32_t ev[4] = {ec.x, ec.y, ec.z, ec.w};
-            uint32_t b0 = 0, b1 = 0;
+            // Weights by the double estimate of softmax_weight_fast; a key
+            // whose estimate lies near a rounding tie, or whose weight needs
+            // the large-weight carry, is flagged and redone below (rare: the
+            // lanes skip that code together when none is flagged).
+            int32_t w[4];
+            uint32_t slow = 0;
 #pragma unroll
             for (int i = 0; i < 4; i++) {
-                const uint64_t e = ev[i] == 0xffffffffu ? (uint64_t)dn::ONE_ACC : ev[i];
-                int32_t w = dn::softmax_weight_fast(e, sum, w_scale, q_scale);
-                wsum += w;
-                if (w >= BIG_WEIGHT) {
-                    const int32_t key = (int32_t)(kt * 16 + 4 * grp + i);
-                    if (big[0] < 0) big[0] = key;
-                    else big[1] = key;
-                    w -= 65536;
-                }
-                const uint32_t u = (uint32_t)(w + 0x8080);  // two digits, each biased by 0x80
-                b0 |= ((u & 0xff) ^ 0x80) << (8 * i);
-                b1 |= (((u >> 8) & 0xff) ^ 0x80) << (8 * i);
+                const double ed = ev[i] == 0xffffffffu ? 4294967296.0 : (double)ev[i];
+                const double t = ed * w_scale + 0.5;
+                const double fl = floor(t);
+                w[i] = (int32_t)fl;
+                slow |= (uint32_t)((fabs(t - fl - 0.5) > 0.5 - 0x1p-15) | (w[i] >= BIG_WEIGHT)) << i;
             }
+            if (slow) {
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    if (!((slow >> i) & 1)) continue;
+                    const uint64_t e = ev[i] == 0xffffffffu ? (uint64_t)dn::ONE_ACC : ev[i];
+                    w[i] = dn::softmax_weight_fast(e, sum, w_scale, q_scale);
+                    if (w[i] >= BIG_WEIGHT) {
+                        const int32_t key = (int32_t)(kt * 16 + 4 * grp + i);
+                        if (big[0] < 0) big[0] = key;
+                        else big[1] = key;
+                        w[i] -= 65536;
+                        wsum += 65536;
+                    }
+                }
+            }
+            wsum += w[0] + w[1] + w[2] + w[3];
+            // Two signed digits per weight: (w + 0x8080) ^ 0x8080 holds
+            // digit 0 in byte 0 and digit 1 in byte 1; byte i of b0 (b1) is
+            // digit 0 (1) of key i.
+            uint32_t d[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) d[i] = (uint32_t)(w[i] + 0x8080) ^ 0x8080u;
+            const uint32_t lo = __builtin_amdgcn_perm(d[1], d[0], 0x05010400u);
+            const uint32_t hi = __builtin_amdgcn_perm(d[3], d[2], 0x05010400u);
+            const uint32_t b0 = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+            const uint32_t b1 = __builtin_amdgcn_perm(hi, lo, 0x07060302u);
             wf0 = v4i{wf0[1], wf0[2], wf0[3], (int)b0};
             wf1 = v4i{wf1[1], wf1[2], wf1[3], (int)b1};
         }

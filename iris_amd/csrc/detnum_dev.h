@@ -29,12 +29,17 @@ __device__ __forceinline__ int64_t sat_neg_i64(int64_t v) { return v == INT64_MI
 
 // ops.rs:773-803. Round-half-even of x / 2^shift; the floor form below is the
 // same rounding as the reference's truncate-then-step form.
+//
+// Every ties-to-even step in this file is written as one comparison,
+// rem + (q & 1) > half (the remainder above half, or at half with q odd),
+// which compiles to a select; the two-clause form became divergent branches
+// with exec-mask bookkeeping around each rounding.
 __device__ __forceinline__ int64_t rshift_rte(int64_t x, uint32_t shift) {
     if (shift == 0) return x;
-    int64_t fl = x >> shift;
-    uint64_t rem = (uint64_t)x & ((((uint64_t)1) << shift) - 1);
-    uint64_t half = (uint64_t)1 << (shift - 1);
-    return (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+    const int64_t fl = x >> shift;
+    const uint64_t rem = (uint64_t)x & ((((uint64_t)1) << shift) - 1);
+    const uint64_t half = (uint64_t)1 << (shift - 1);
+    return fl + (int64_t)(rem + (uint64_t)(fl & 1) > half);
 }
 
 // ops.rs:448-451 + :483-486
@@ -90,10 +95,9 @@ __device__ __forceinline__ int32_t div_act(int32_t n, int32_t d) {
 // ops.rs:685-689: round-half-even of a*b / 2^32, clamped.
 __device__ __forceinline__ int64_t acc_mul(int64_t a, int64_t b) {
     i128 p = (i128)a * (i128)b;
-    i128 fl = p >> 32;
-    uint64_t rem = (uint64_t)p & 0xffffffffull;
-    const uint64_t half = 0x80000000ull;
-    i128 r = (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+    const i128 fl = p >> 32;
+    const uint64_t rem = (uint64_t)p & 0xffffffffull;
+    const i128 r = fl + (i128)(rem + (uint64_t)(fl & 1) > 0x80000000ull);
     return clamp_i128_to_i64(r);
 }
 
@@ -199,20 +203,17 @@ __device__ __forceinline__ int32_t rms_scale_from_sum(int64_t sum_squares, uint3
 
 // rte(x / c) (ops.rs:691-720) for a non-negative dividend below 2^32.
 __device__ __forceinline__ uint32_t rte_div_u32(uint32_t x, uint32_t c) {
-    uint32_t q = x / c;
-    const uint32_t twice = 2 * (x - q * c);
-    if (twice > c || (twice == c && (q & 1))) q++;
-    return q;
+    const uint32_t q = x / c;
+    return q + (uint32_t)(2 * (x - q * c) + (q & 1) > c);
 }
 
 // acc_mul (ops.rs:685-689) of 0 <= a, b < 2^32: the product fits 64 bits,
 // and the rounded result stays below 2^32 when a or b is below 2^32 - 1.
+// (p + 2^31 - 1 + (floor & 1)) carries into the high word exactly when the
+// rounding steps up; p <= (2^32 - 1)^2 leaves room for the addend.
 __device__ __forceinline__ uint32_t acc_mul_u32(uint32_t a, uint32_t b) {
     const uint64_t p = (uint64_t)a * b;
-    uint32_t fl = (uint32_t)(p >> 32);
-    const uint32_t rem = (uint32_t)p;
-    if (rem > 0x80000000u || (rem == 0x80000000u && (fl & 1))) fl++;
-    return fl;
+    return (uint32_t)((p + 0x7fffffffull + ((p >> 32) & 1)) >> 32);
 }
 
 // softmax_exp_term (ops.rs:508-556) of delta = -(diff << 16), diff >= 0:
@@ -224,20 +225,19 @@ __device__ __forceinline__ uint32_t acc_mul_u32(uint32_t a, uint32_t b) {
 // so the general routine's integers come out of 32-bit operations. The
 // quotient by ln 2 starts from a float estimate (off by at most one, as
 // diff < 2^20 is exact in a float) and is corrected on the remainder.
+// The body is branch-free (selects only), so a wave's lanes run it together.
 __device__ __forceinline__ uint64_t softmax_exp_diff(uint32_t diff) {
     if (diff >= (1u << 20)) return 0;
-    if (diff == 0) return (uint64_t)ONE_ACC;
     const int64_t LN_2_BITS = 2977044472LL;
     const int64_t positive = (int64_t)diff << 16;
     uint32_t shift = (uint32_t)((float)diff * (65536.0f / 2977044472.0f));
     int64_t rl = positive - (int64_t)shift * LN_2_BITS;
-    if (rl < 0) {
-        shift--;
-        rl += LN_2_BITS;
-    } else if (rl >= LN_2_BITS) {
-        shift++;
-        rl -= LN_2_BITS;
-    }
+    const bool below = rl < 0;
+    shift -= (uint32_t)below;
+    rl += below ? LN_2_BITS : 0;
+    const bool above = rl >= LN_2_BITS;
+    shift += (uint32_t)above;
+    rl -= above ? LN_2_BITS : 0;
     const uint32_t r = (uint32_t)rl;
     const uint32_t r2 = acc_mul_u32(r, r), r3 = acc_mul_u32(r2, r);
     const uint32_t r4 = acc_mul_u32(r3, r), r5 = acc_mul_u32(r4, r);
@@ -245,11 +245,11 @@ __device__ __forceinline__ uint64_t softmax_exp_diff(uint32_t diff) {
     // in (0, 2^32)).
     const uint32_t approx = 0u - r + rte_div_u32(r2, 2) - rte_div_u32(r3, 6) + rte_div_u32(r4, 24) -
                             rte_div_u32(r5, 120);
-    if (shift == 0) return approx;
-    uint32_t fl = approx >> shift;
-    const uint32_t rem = approx & ((1u << shift) - 1), half = 1u << (shift - 1);
-    if (rem > half || (rem == half && (fl & 1))) fl++;
-    return fl;
+    const uint32_t fl = approx >> shift;
+    const uint32_t rem = approx & ((1u << shift) - 1), half = (1u << shift) >> 1;
+    const uint32_t rounded = fl + (uint32_t)(rem + (fl & 1) > half);
+    // diff = 0: r = 0 and the sum is 2^32, which wraps to 0 above.
+    return diff == 0 ? (uint64_t)ONE_ACC : (uint64_t)(shift == 0 ? approx : rounded);
 }
 
 // attention_softmax_raw_weight (ops.rs:269-271), requantize(div_acc(e, sum)),
@@ -285,8 +285,8 @@ __device__ __forceinline__ int32_t softmax_weight(uint64_t e, uint64_t sum, doub
 __device__ __forceinline__ int32_t softmax_weight_fast(uint64_t e, uint64_t sum, double w_scale, double q_scale) {
     const double t = (double)e * w_scale + 0.5;
     const double fl = floor(t);
-    const double f = t - fl;
-    if (f < 0x1p-15 || f > 1.0 - 0x1p-15) return softmax_weight(e, sum, q_scale);
+    // The fraction t - fl below 2^-15 or above 1 - 2^-15, as one comparison.
+    if (fabs(t - fl - 0.5) > 0.5 - 0x1p-15) return softmax_weight(e, sum, q_scale);
     return (int32_t)fl;
 }
 
@@ -351,10 +351,10 @@ __device__ inline void sin_cos_acc(int64_t angle, int32_t& cos_out, int32_t& sin
 
 // mistral.rs:23-32
 __device__ __forceinline__ int64_t m_shift_rte(int64_t value, uint32_t shift) {
-    int64_t fl = value >> shift;
-    int64_t rem = value - (int64_t)((uint64_t)fl << shift);
-    int64_t half = (int64_t)1 << (shift - 1);
-    return (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+    const int64_t fl = value >> shift;
+    const int64_t rem = value - (int64_t)((uint64_t)fl << shift);
+    const int64_t half = (int64_t)1 << (shift - 1);
+    return fl + (int64_t)(rem + (fl & 1) > half);
 }
 
 // mistral.rs:43-56. r < ln 2 < 2^32 and acc <= 2^32 throughout, so each
@@ -459,10 +459,10 @@ __device__ __forceinline__ int32_t scaled_score_from_sum(int64_t sum, uint32_t s
 
 // q8.rs:94-104: value / 2^shift, ties to even, saturated to i32.
 __device__ __forceinline__ int32_t round_to_i32(i128 value, uint32_t shift) {
-    i128 fl = value >> shift;
-    i128 rem = value - (fl << shift);
-    i128 half = (i128)1 << (shift - 1);
-    i128 r = (rem > half || (rem == half && (fl & 1))) ? fl + 1 : fl;
+    const i128 fl = value >> shift;
+    const uint64_t rem = (uint64_t)(value - (fl << shift));  // in [0, 2^shift), shift < 64
+    const uint64_t half = (uint64_t)1 << (shift - 1);
+    const i128 r = fl + (i128)(rem + (uint64_t)(fl & 1) > half);
     return clamp_i128_to_i32(r);
 }
 
