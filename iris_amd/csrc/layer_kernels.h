@@ -46,6 +46,9 @@ struct AttnArgs {
     int scaled;              // 1: mistral scaled_score; 0: gemma requantized dot
     uint32_t scale_q32;
     uint32_t window;         // 0 = every earlier position is visible
+    // One-row launches: the head's scores between the two decode kernels,
+    // [heads][k_pos_stride] (null: the one-workgroup-per-head kernel).
+    int32_t* scores;
     // Digit planes for the multi-row MFMA path (planes.q null: the scalar
     // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes /
     // attn_e_store_bytes.

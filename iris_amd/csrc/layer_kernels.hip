@@ -12,20 +12,72 @@ __global__ __launch_bounds__(ATTN_MAX_THREADS) void attention_kernel(const AttnA
     attend_row(a, blockIdx.x, blockIdx.y, sm);
 }
 
-// One query row in one launch. Every workgroup of a head recomputes the
-// head's scores (the key loads of a round issued together), its first
-// maximum, exp terms and
-// weights, then forms the weighted values of its own 32-dimension slice over
-// every key, the slice's value loads issued before the softmax so they are
-// in flight while it runs. No partials cross workgroups: nothing to combine.
+// One query row in two launches. (1) attn_scores_kernel: one workgroup per
+// (query head, 64-position chunk of the cache) forms the chunk's scores
+// (wrapping i64 dot, then scaled_score or requantize) into a.scores; each
+// workgroup reads only its chunk's keys, so the key bytes a head needs are
+// spread over many compute units. (2) attn_values_kernel: one workgroup per
+// (query head, 32-dimension slice) reads the head's scores, finds the first
+// maximum, forms the exp terms, their sum and the weights, then the weighted
+// values of its slice over every key; the slice's value loads are issued
+// first and stay in flight through the softmax.
+
+// Thread (position quad kq, dimension group grp of 16) holds HD/16 dimensions
+// of four consecutive positions: one 16-byte load per dimension from the
+// transposed cache (consecutive lanes read consecutive positions of one
+// dimension); the groups' partial sums meet by shuffles, then across the
+// four waves in LDS.
 template <uint32_t HD>
-__global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
+    constexpr uint32_t DPG = HD / 16;
+    __shared__ int32_t s_q[HD];
+    __shared__ uint64_t s_part[4][64];
+    const uint32_t head = blockIdx.x, c0 = blockIdx.y * 64, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t pos = (uint32_t)(*a.d_pos);
+    const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
+    if (c0 > pos || c0 + 63 < start) return;  // the chunk holds no visible key
+    const uint32_t kvh = head / (a.heads / a.kv_heads);
+    // The query element this thread stages, loaded first (waiting for it
+    // does not wait for the key loads issued after it).
+    const int32_t qv = a.q[(size_t)head * HD + tid % HD];
+    const uint32_t kq = lane & 15, grp = wave * 4 + (lane >> 4);
+    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + grp * DPG) * a.k_pos_stride + c0 + 4 * kq;
+    int4 kv[DPG];
+#pragma unroll
+    for (uint32_t i = 0; i < DPG; i++) kv[i] = *(const int4*)(kb + (size_t)i * a.k_pos_stride);
+    if (tid < HD) s_q[tid] = qv;
+    lds_barrier();
+    uint64_t dot[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (uint32_t i = 0; i < DPG; i++) {
+        const int64_t q = s_q[grp * DPG + i];
+        dot[0] += (uint64_t)(q * kv[i].x);
+        dot[1] += (uint64_t)(q * kv[i].y);
+        dot[2] += (uint64_t)(q * kv[i].z);
+        dot[3] += (uint64_t)(q * kv[i].w);
+    }
+#pragma unroll
+    for (uint32_t off = 16; off < 64; off <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; c++) dot[c] += __shfl_xor(dot[c], off);
+    if (lane < 16)
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_part[wave][4 * kq + c] = dot[c];
+    lds_barrier();
+    if (tid < 64) {
+        const uint64_t sum = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+        const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)sum, a.scale_q32) : dn::requantize((int64_t)sum);
+        a.scores[(size_t)head * a.k_pos_stride + c0 + tid] = sc;  // positions outside the view are never read
+    }
+}
+
+template <uint32_t HD>
+__global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
     constexpr uint32_t NT = 512, NWV = NT / 64;
     constexpr uint32_t DS = 32;                             // dimensions per workgroup
     constexpr uint32_t VR = 16;                             // 64-key value rounds loaded before the softmax
-    constexpr uint32_t EPT = ATTN_MAX_KEYS / NT;            // exp terms per thread, at most
-    __shared__ int32_t s_w[ATTN_MAX_KEYS];                  // scores, then weights
-    __shared__ int32_t s_q[HD];
+    constexpr uint32_t EPT = ATTN_MAX_KEYS / NT;            // keys per thread, at most
+    __shared__ int32_t s_w[ATTN_MAX_KEYS];                  // weights
     __shared__ int64_t s_part[64 * DS];
     __shared__ ArgMax s_am[NWV];
     __shared__ uint64_t s_sum[NWV];
@@ -35,58 +87,17 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
     const uint32_t n = pos - start + 1;
-    for (uint32_t d = tid; d < HD; d += NT) s_q[d] = a.q[(size_t)head * HD + d];
-    __syncthreads();
 
-    // 1. Scores (wrapping i64 dot, then scaled_score or requantize) and the
-    // first maximum. Thread (dimension group g of NDG, key quad kq) holds the
-    // 32 dimensions 32g.. of four consecutive positions, one 16-byte load per
-    // dimension from the transposed cache (its position stride is a multiple
-    // of 64; consecutive lanes read consecutive positions of one dimension);
-    // the groups' partial sums meet by shuffles. Positions run in increasing
-    // order in each thread.
-    constexpr uint32_t NDG = HD / 32, QPW = 64 / NDG, KPR = 4 * QPW * NWV;  // positions per round
-    const uint32_t g = lane / QPW, kq = wave * QPW + lane % QPW;
-    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + 32 * g) * a.k_pos_stride;
-    const uint32_t p0 = start & ~3u;
-    ArgMax best{INT32_MIN, 0xffffffffu};
-    for (uint32_t pb = p0; pb <= pos; pb += KPR) {
-        const uint32_t p = pb + 4 * kq, safe = p <= pos ? p : p0;
-        int4 kv[32];
+    // 1. This thread's scores (keys tid + NT*u, increasing), then the slice's
+    // value rows; both loads are unconditional (clamped indices), the scores
+    // first so that waiting for them does not wait for the values.
+    const int32_t* sb = a.scores + (size_t)head * a.k_pos_stride + start;
+    int32_t sc[EPT];
 #pragma unroll
-        for (uint32_t i = 0; i < 32; i++) kv[i] = *(const int4*)(kb + (size_t)i * a.k_pos_stride + safe);
-        uint64_t dot[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (uint32_t i = 0; i < 32; i++) {
-            const int64_t q = s_q[32 * g + i];
-            dot[0] += (uint64_t)(q * kv[i].x);
-            dot[1] += (uint64_t)(q * kv[i].y);
-            dot[2] += (uint64_t)(q * kv[i].z);
-            dot[3] += (uint64_t)(q * kv[i].w);
-        }
-#pragma unroll
-        for (uint32_t off = QPW; off < 64; off <<= 1)
-#pragma unroll
-            for (int c = 0; c < 4; c++) dot[c] += __shfl_xor(dot[c], off);
-        // Every group holds the four sums now; group g scores positions
-        // CPL*g.. of the quad.
-        constexpr uint32_t CPL = NDG >= 4 ? 1 : 4 / NDG;
-#pragma unroll
-        for (uint32_t c = 0; c < 4; c++) {
-            const uint32_t at = p + c;
-            if (c / CPL == g && at >= start && at <= pos) {
-                const uint32_t key = at - start;
-                const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)dot[c], a.scale_q32)
-                                            : dn::requantize((int64_t)dot[c]);
-                s_w[key] = sc;
-                best = argmax_combine(best, ArgMax{sc, key});
-            }
-        }
+    for (uint32_t u = 0; u < EPT; u++) {
+        const uint32_t j = tid + NT * u;
+        sc[u] = sb[j < n ? j : 0];
     }
-    best = wave_argmax(best);
-    if (lane == 0) s_am[wave] = best;
-
-    // 2. This slice's value rows, loaded now, used after the softmax.
     const uint32_t kr = tid / 8, d4 = (tid % 8) * 4;
     const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * HD + slice * DS + d4;
     int4 vv[VR];
@@ -95,7 +106,17 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
         const uint32_t key = kr + 64 * r;
         vv[r] = *(const int4*)(vb + (size_t)(key < n ? key : 0) * a.kv_stride);
     }
-    __syncthreads();
+
+    // 2. The first maximum.
+    ArgMax best{INT32_MIN, 0xffffffffu};
+#pragma unroll
+    for (uint32_t u = 0; u < EPT; u++) {
+        const uint32_t j = tid + NT * u;
+        if (j < n) best = argmax_combine(best, ArgMax{sc[u], j});
+    }
+    best = wave_argmax(best);
+    if (lane == 0) s_am[wave] = best;
+    lds_barrier();  // the value loads stay in flight
     ArgMax m = s_am[0];
     for (uint32_t i = 1; i < NWV; i++) m = argmax_combine(m, s_am[i]);
 
@@ -106,16 +127,14 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
 #pragma unroll
     for (uint32_t u = 0; u < EPT; u++) {
         const uint32_t j = tid + NT * u;
+        const int64_t diff = (int64_t)m.v - sc[u];
         ev[u] = 0;
-        if (j < n) {
-            const int64_t diff = (int64_t)m.v - s_w[j];
-            ev[u] = dn::softmax_exp_diff((uint32_t)(diff > (1 << 20) ? (1 << 20) : diff));
-        }
+        if ((j < n) & (diff < (1 << 20))) ev[u] = dn::softmax_exp_diff((uint32_t)diff);
         part += ev[u];
     }
     for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
     if (lane == 0) s_sum[wave] = part;
-    __syncthreads();
+    lds_barrier();
     uint64_t total = 0;
     for (uint32_t i = 0; i < NWV; i++) total += s_sum[i];
     const double w_scale = 65536.0 / (double)total, q_scale = 4294967296.0 / (double)total;
@@ -131,7 +150,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     }
     wpart = wave_sum_sat32(wpart);
     if (lane == 0) s_wsum[wave] = wpart;
-    __syncthreads();
+    lds_barrier();
     int32_t wsum = 0;
     for (uint32_t i = 0; i < NWV; i++) wsum = dn::add_sat(wsum, s_wsum[i]);
 
@@ -158,7 +177,7 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
     }
 #pragma unroll
     for (int c = 0; c < 4; c++) s_part[kr * DS + d4 + c] = (int64_t)acc[c];
-    __syncthreads();
+    lds_barrier();
     if (tid < DS) {
         uint64_t t = 0;
         for (uint32_t r = 0; r < 64; r++) t += (uint64_t)s_part[r * DS + tid];
@@ -172,7 +191,8 @@ __global__ __launch_bounds__(512) void attn_decode_kernel(const AttnArgs a) {
 
 template <uint32_t HD>
 int attention_decode_launch(const AttnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_decode_kernel<HD>, dim3(a.heads, HD / 32), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(a.heads, a.k_pos_stride / 64), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(attn_values_kernel<HD>, dim3(a.heads, HD / 32), dim3(512), 0, stream, a);
     return (int)hipGetLastError();
 }
 
@@ -235,8 +255,8 @@ int iris_rope_table_launch(const int64_t* inv_freq, uint32_t half, const int32_t
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream) {
     if (a.head_dim > ATTN_MAX_HEAD_DIM || a.head_dim % 4 || max_keys > ATTN_MAX_KEYS || a.heads % a.kv_heads)
         return IRIS_E_INVALID;
-    if (tokens == 1 && a.k_pos_stride % 4 == 0) {
-        // One row: HD/32 workgroups per head, each over every key.
+    if (tokens == 1 && a.scores && a.k_pos_stride % 64 == 0 && max_keys <= a.k_pos_stride) {
+        // One row: the chunked scores, then HD/32 workgroups per head.
         switch (a.head_dim) {
             case 32: return attention_decode_launch<32>(a, stream);
             case 64: return attention_decode_launch<64>(a, stream);

@@ -145,11 +145,6 @@ __device__ __forceinline__ void wait_vmem() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// All of this wave's LDS reads have returned, then every wave meets.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // One pass of the workgroup over the whole k range: RT weight tiles of 32
 // rows (from 32-row tile rt0) times 2*TTW token tiles of 32 (from tt0) times
 // LG digit planes. Wave (wr, wt) accumulates weight tiles wr*2, wr*2+1

@@ -342,12 +342,6 @@ __device__ __forceinline__ int64_t sumsq4(int64_t s, int4 v) {
 
 constexpr uint32_t XROUND = 4;  // int4 loads a thread has in flight per staging round
 
-// Barrier for LDS traffic only: global loads still in flight (the weight
-// prefetch) stay in flight, where __syncthreads would wait for them.
-__device__ __forceinline__ void lds_barrier() {
-    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
 // The persistent kernel's prologue: the row's rms_norm scale when asked
 // (sum of squares: saturating, non-negative terms, so order-free) and every
 // digit plane of the row in LDS. A thread issues XROUND 16-byte loads (with

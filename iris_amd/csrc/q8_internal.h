@@ -125,6 +125,12 @@ struct GemvArgs {
 
 constexpr uint32_t GEMV_SSQ_SLOTS = 256;
 
+// Barrier for LDS traffic only: global loads still in flight (a prefetch)
+// stay in flight, where __syncthreads would wait for every one of them.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Bytes of the MFMA product's digit planes: 5 planes of the tokens rounded
 // up to whole 32-token tiles, times cols, 256-byte aligned.
 inline uint64_t gemm_planes_bytes(uint32_t cols, uint32_t tokens) {

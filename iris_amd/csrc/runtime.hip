@@ -468,6 +468,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         a.scale_q32 = d.attention_scale_q32;
         a.window = 0;
         a.planes = s->attn_planes;
+        a.scores = s->scores;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 3. attended = W_o ctx + x.
         g = GemvArgs{};
@@ -606,6 +607,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         a.scaled = 0;
         a.window = L.window;
         a.planes = s->attn_planes;
+        a.scores = s->scores;
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 4. attended = rms_norm(W_o ctx, post_attention) + x  (:879-892)
         g = GemvArgs{};
@@ -800,6 +802,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     if (st == hipSuccess) st = hipMalloc((void**)&s->ssq_x, GEMV_SSQ_SLOTS * sizeof(int64_t));
     if (st == hipSuccess) st = hipMalloc((void**)&s->ssq_att, GEMV_SSQ_SLOTS * sizeof(int64_t));
     alloc(&s->q, (size_t)max_rows * qw);
+    alloc(&s->scores, (size_t)d.heads * s->k_pos_stride);
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
     if (max_rows > 1) {
@@ -846,7 +849,7 @@ void iris_session_free(IrisSession* s) {
     if (s->graph_exec) hipGraphExecDestroy(s->graph_exec);
     for (auto p : s->k_cache) hipFree(p);
     for (auto p : s->v_cache) hipFree(p);
-    for (int32_t* p : {s->x, s->attended, s->q, s->ctx, s->gated, s->logits, s->ids, s->tokens, s->d_pos, s->d_step,
+    for (int32_t* p : {s->x, s->attended, s->q, s->scores, s->ctx, s->gated, s->logits, s->ids, s->tokens, s->d_pos, s->d_step,
                        s->logits_keep, s->qkv, s->tmp, s->ple_proj, s->ple_rows, s->ple_gated})
         hipFree(p);
     hipFree(s->sel_partial);

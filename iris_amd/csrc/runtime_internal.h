@@ -68,6 +68,7 @@ struct IrisSession {
     hipStream_t stream = nullptr;
     std::vector<int32_t*> k_cache, v_cache;  // per layer [position][kv_heads*head_dim]
     int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;
+    int32_t* scores = nullptr;  // one-row attention: [heads][k_pos_stride]
     // One-row passes: per-tile sums of squares of x and attended, written by
     // the residual products and read by the norms that follow them.
     int64_t *ssq_x = nullptr, *ssq_att = nullptr;
@@ -85,7 +86,6 @@ struct IrisSession {
     size_t logits_keep_cap = 0;
     bool keep_logits = false;
     uint64_t* sel_partial = nullptr;
-    // split decode attention scratch
     int64_t* rope_sc = nullptr;      // mistral-dense: [max_rows][head_dim/2][sin, cos] of the pass's positions
     // multi-row attention digit planes (null for single-row sessions)
     AttnPlanes attn_planes{};
