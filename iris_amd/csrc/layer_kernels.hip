@@ -3,6 +3,7 @@
 #include "attn_common.h"
 #include "detnum_dev.h"
 #include "layer_kernels.h"
+#include "wave_ops.h"
 
 namespace {
 
@@ -107,15 +108,18 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
         vv[r] = *(const int4*)(vb + (size_t)(key < n ? key : 0) * a.kv_stride);
     }
 
-    // 2. The first maximum.
-    ArgMax best{INT32_MIN, 0xffffffffu};
+    // 2. The first maximum, as the largest key (score with its sign bit
+    // flipped, then the complemented index: equal scores favour the lower
+    // index; 0 = no key).
+    uint64_t best = 0;
 #pragma unroll
     for (uint32_t u = 0; u < EPT; u++) {
         const uint32_t j = tid + NT * u;
-        if (j < n) best = argmax_combine(best, ArgMax{sc[u], j});
+        const uint64_t k = ((uint64_t)((uint32_t)sc[u] ^ 0x80000000u) << 32) | (uint32_t)~j;
+        best = (j < n) & (k > best) ? k : best;
     }
-    best = wave_argmax(best);
-    if (lane == 0) s_am[wave] = best;
+    best = wave_max_u64(best);
+    if (lane == 0) s_am[wave] = ArgMax{(int32_t)((uint32_t)(best >> 32) ^ 0x80000000u), ~(uint32_t)best};
     lds_barrier();  // the value loads stay in flight
     ArgMax m = s_am[0];
     for (uint32_t i = 1; i < NWV; i++) m = argmax_combine(m, s_am[i]);
@@ -132,7 +136,7 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
         if ((j < n) & (diff < (1 << 20))) ev[u] = dn::softmax_exp_diff((uint32_t)diff);
         part += ev[u];
     }
-    for (int off = 32; off >= 1; off >>= 1) part += __shfl_xor(part, off);
+    part = wave_sum_u64(part);
     if (lane == 0) s_sum[wave] = part;
     lds_barrier();
     uint64_t total = 0;
@@ -148,7 +152,9 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
             wpart += w;
         }
     }
-    wpart = wave_sum_sat32(wpart);
+    // Weights are non-negative and at most 4096 * 2^16 in all: the
+    // saturating sum never saturates, a plain sum is the same.
+    wpart = (int32_t)wave_sum_u64((uint64_t)(uint32_t)wpart);
     if (lane == 0) s_wsum[wave] = wpart;
     lds_barrier();
     int32_t wsum = 0;

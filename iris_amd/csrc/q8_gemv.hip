@@ -15,6 +15,7 @@
 #include "detnum_dev.h"
 #include "q8_internal.h"
 #include "q8_epilogue.h"
+#include "wave_ops.h"
 
 namespace {
 
@@ -30,40 +31,6 @@ __device__ __forceinline__ uint64_t digits5(int32_t v) {
 
 __device__ __forceinline__ int limbs_needed(uint64_t d) {
     return (d >> 32) ? 5 : (d >> 24) ? 4 : (d >> 16) ? 3 : (d >> 8) ? 2 : 1;
-}
-
-// A 64-bit value from another lane of the same 16-lane row (DPP control
-// CTRL: a register move, no LDS round trip).
-template <int CTRL>
-__device__ __forceinline__ int64_t dpp64(int64_t v) {
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)v, CTRL, 0xF, 0xF, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(uint32_t)((uint64_t)v >> 32), CTRL, 0xF, 0xF, false);
-    return (int64_t)(((uint64_t)(uint32_t)hi << 32) | (uint32_t)lo);
-}
-
-// Saturating sum of non-negative terms over each 16-lane row, in every lane
-// of the row: min(true sum, i64::MAX), the same in any order. Lanes swap
-// within quads (1, then 2 apart), then mirror within half rows and rows.
-// Every lane of the wave must be active.
-__device__ __forceinline__ int64_t row16_sum_sat_nonneg(int64_t v) {
-    v = dn::acc_add_sat(v, dpp64<0xB1>(v));   // quad_perm [1,0,3,2]
-    v = dn::acc_add_sat(v, dpp64<0x4E>(v));   // quad_perm [2,3,0,1]
-    v = dn::acc_add_sat(v, dpp64<0x141>(v));  // row_half_mirror
-    v = dn::acc_add_sat(v, dpp64<0x140>(v));  // row_mirror
-    return v;
-}
-
-// The same over the whole wave: the four row sums through scalar registers.
-__device__ __forceinline__ int64_t wave_sum_sat_nonneg(int64_t v) {
-    v = row16_sum_sat_nonneg(v);
-    int64_t t = 0;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, 16 * r);
-        const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), 16 * r);
-        t = dn::acc_add_sat(t, (int64_t)(((uint64_t)hi << 32) | lo));
-    }
-    return t;
 }
 
 __device__ __forceinline__ int wave_max_int(int v) {
