@@ -318,12 +318,7 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
 #pragma unroll 1
     for (uint32_t ks = ks0; ks < ks1; ks++) {
         // The step's value operands, needed after its four weight tiles.
-        v4i vf[DT][AP_V_PLANES];
         const int8_t* vb = vbase + (size_t)ks * DT * FRAG;
-#pragma unroll
-        for (uint32_t dt = 0; dt < DT; dt++)
-#pragma unroll
-            for (int b = 0; b < AP_V_PLANES; b++) vf[dt][b] = *(const v4i*)(vb + b * vl + dt * FRAG);
         // The two weight digits of this lane's 16 keys: byte 4t + i of wf0/wf1
         // (tile t is shifted in as the last component).
         v4i wf0 = v4i{0, 0, 0, 0}, wf1 = v4i{0, 0, 0, 0};
@@ -377,12 +372,16 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
             wf1 = v4i{wf1[1], wf1[2], wf1[3], (int)b1};
         }
 #pragma unroll
-        for (uint32_t dt = 0; dt < DT; dt++)
+        for (uint32_t dt = 0; dt < DT; dt++) {
+            v4i vf[AP_V_PLANES];
+#pragma unroll
+            for (int b = 0; b < AP_V_PLANES; b++) vf[b] = *(const v4i*)(vb + b * vl + dt * FRAG);
 #pragma unroll
             for (int b = 0; b < AP_V_PLANES; b++) {
-                pacc[dt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf0, vf[dt][b], pacc[dt][b], 0, 0, 0);
-                pacc[dt][b + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf1, vf[dt][b], pacc[dt][b + 1], 0, 0, 0);
+                pacc[dt][b] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf0, vf[b], pacc[dt][b], 0, 0, 0);
+                pacc[dt][b + 1] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf1, vf[b], pacc[dt][b + 1], 0, 0, 0);
             }
+        }
     }
     wsum += __shfl_xor(wsum, 16);
     wsum += __shfl_xor(wsum, 32);
@@ -424,7 +423,7 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
 }
 
 template <uint32_t HD>
-__global__ __launch_bounds__(256, 1) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
+__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
     __shared__ union {
         AttnRowSmem row;
         PrefillSmem pre;
