@@ -12,9 +12,9 @@
 //
 // The softmax needs each row's first maximum before any exp term and the
 // full sum before any weight, so each workgroup walks its keys three times:
-// (1) scores and the first maximum; (2) scores again (cheap on the matrix
-// cores), the exp terms and their sum, the terms kept in an HBM store;
-// (3) the weights from the stored terms and the weighted values. The
+// (1) scores and the first maximum, the scores kept in an HBM store; (2) the
+// exp terms of the stored scores and their sum, the terms overwriting the
+// scores; (3) the weights from the stored terms and the weighted values. The
 // weights never leave registers: the score tile's lane layout is, up to a
 // fixed permutation of the keys inside each 64-key step, the A operand of
 // the value product, and the value planes are written in that permuted key
@@ -239,7 +239,9 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
     const uint32_t kt0 = ks0 * 4, kt1 = ks1 * 4;  // 16-key tiles
     v4i kf[LQK][DS], kn[LQK][DS];
 
-    // (1) the first maximum: keys run in increasing order in each lane.
+    // (1) the scores, kept in the exp store (one 16-byte slot per lane and
+    // tile), and the first maximum: keys run in increasing order in each lane.
+    uint32_t* estore = p.e_store + ((size_t)head * p.qt_cap + qt) * p.ks_cap * 4 * 256 + lane * 4;
     int32_t best = INT32_MIN;
     uint32_t best_key = 0xffffffffu;
     load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
@@ -248,6 +250,7 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
         if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
         int32_t sc[4];
         tile_scores<HD, LQK>(a, kf, qf, sc);
+        *(uint4*)(estore + (size_t)kt * 256) = make_uint4((uint32_t)sc[0], (uint32_t)sc[1], (uint32_t)sc[2], (uint32_t)sc[3]);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const uint32_t key = kt * 16 + 4 * grp + i;
@@ -270,18 +273,17 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
         }
     }
 
-    // (2) the sum of exp terms (non-negative, so no order and no saturation);
-    // each lane keeps its terms for (3) in the exp store, one 16-byte slot
-    // per tile (2^32, the maximum's term, as 0xffffffff: every other term is
-    // below 2^32 - 2^15).
+    // (2) the sum of exp terms (non-negative, so no order and no saturation)
+    // from the stored scores; each lane overwrites a tile's scores with its
+    // terms for (3) (2^32, the maximum's term, as 0xffffffff: every other
+    // term is below 2^32 - 2^15).
     uint64_t sum = 0;
-    uint32_t* estore = p.e_store + ((size_t)head * p.qt_cap + qt) * p.ks_cap * 4 * 256 + lane * 4;
-    load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+    uint4 sn = *(const uint4*)(estore + (size_t)kt0 * 256);
 #pragma unroll 1
     for (uint32_t kt = kt0; kt < kt1; kt++) {
-        if (kt + 1 < kt1) load_key_tile<HD, LQK>(kbase + (size_t)(kt + 1) * DS * FRAG, kl, kn);
-        int32_t sc[4];
-        tile_scores<HD, LQK>(a, kf, qf, sc);
+        const uint4 scv = sn;
+        if (kt + 1 < kt1) sn = *(const uint4*)(estore + (size_t)(kt + 1) * 256);
+        const int32_t sc[4] = {(int32_t)scv.x, (int32_t)scv.y, (int32_t)scv.z, (int32_t)scv.w};
         uint32_t ev[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -293,10 +295,6 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
             ev[i] = e > 0xffffffffull ? 0xffffffffu : (uint32_t)e;
         }
         *(uint4*)(estore + (size_t)kt * 256) = make_uint4(ev[0], ev[1], ev[2], ev[3]);
-#pragma unroll
-        for (int l = 0; l < LQK; l++)
-#pragma unroll
-            for (uint32_t ds = 0; ds < DS; ds++) kf[l][ds] = kn[l][ds];
     }
     sum += __shfl_xor(sum, 16);
     sum += __shfl_xor(sum, 32);
