@@ -94,7 +94,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path (run with --gpus 1)",
+        print("bench.py measures one MI355X: the library has no multi-GPU path (run with --gpus 1)",
               file=sys.stderr)
         sys.exit(2)
     if args.steps < 1 or PROMPT + args.steps > 4096:

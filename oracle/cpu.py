@@ -2,7 +2,7 @@
 loop restated over them.
 
 TEST INFRASTRUCTURE ONLY. Tests, ``__graft_entry__.smoke()`` and the
-benchmark's ``cpu_baseline`` leg use this as the checker / CPU baseline; the
+benchmark's ``cpu_baseline`` leg use this as the expected result / CPU baseline; the
 shipped package never imports it.
 
 The loop follows crates/inference/direct/src/executor.rs:143-185 (prefill all

@@ -2,8 +2,8 @@
  * CPU oracle: a plain-C restatement of iris's det-num fixed-point arithmetic
  * (crates/det-num) and of the layer kernels built on it.
  *
- * TEST INFRASTRUCTURE ONLY. This code is the checker the HIP path is compared
- * against, and the timed CPU baseline. Nothing in the shipped library links,
+ * TEST INFRASTRUCTURE ONLY. This code gives the expected results the HIP path is
+ * compared against, and the timed CPU baseline. Nothing in the shipped library links,
  * loads or calls it; only tests, the smoke check and the benchmark's CPU
  * baseline leg do.
  *
