@@ -284,11 +284,28 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
             if (2 * pair < w.rows && token < a.tokens) a.out[(size_t)token * a.out_stride + pair] = sC[pl * STRIDE + tl];
         }
     } else {
-        for (uint32_t c = tid; c < ROWS * NTOK; c += G::THREADS) {
-            const uint32_t rl = c % ROWS, tl = c / ROWS;
-            const uint32_t row = rt0 * 32 + rl, token = tt0 * 32 + tl;
-            if (row < w.rows && token < a.tokens)
-                store_output(a, row, token, sC[rl * STRIDE + tl], sC[(rl ^ 1) * STRIDE + tl]);
+        // One loop per epilogue (the choice is uniform), each reading only
+        // what its epilogue uses.
+        auto each = [&](auto&& f) __attribute__((always_inline)) {
+            for (uint32_t c = tid; c < ROWS * NTOK; c += G::THREADS) {
+                const uint32_t rl = c % ROWS, tl = c / ROWS;
+                const uint32_t row = rt0 * 32 + rl, token = tt0 * 32 + tl;
+                if (row < w.rows && token < a.tokens) f(row, token, sC[rl * STRIDE + tl], sC[(rl ^ 1) * STRIDE + tl]);
+            }
+        };
+        if (a.epilogue == EPI_RESIDUAL) {
+            each([&](uint32_t row, uint32_t token, int32_t v, int32_t) __attribute__((always_inline)) {
+                a.out[(size_t)token * a.out_stride + row] =
+                    dn::add_sat(v, a.residual[(size_t)token * a.residual_stride + row]);
+            });
+        } else if (a.epilogue == EPI_ROPE_KV) {
+            each([&](uint32_t row, uint32_t token, int32_t v, int32_t partner) __attribute__((always_inline)) {
+                store_output(a, row, token, v, partner);
+            });
+        } else {
+            each([&](uint32_t row, uint32_t token, int32_t v, int32_t partner) __attribute__((always_inline)) {
+                store_output_in(a, row, token, v, partner, EpiIn{0, 0, 0, 0});
+            });
         }
     }
     __syncthreads();
