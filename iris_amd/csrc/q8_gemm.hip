@@ -251,13 +251,33 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
         for (int j = 0; j < TTW; j++) {
             const uint32_t tl = (wt * TTW + j) * 32 + (lane & 31);
             int32_t v[16];
+            // round_to_i32(tot * scale, 24) (q8.rs:94-104) through one 64-bit
+            // product where the operands' bit lengths show it cannot
+            // overflow (the usual case); if any lane of the wave has a
+            // larger product, the wave redoes the block with 128-bit ones.
+            bool fits = true;
 #pragma unroll
             for (int e = 0; e < 16; e++) {
                 const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4), row = rt0 * 32 + rl;
                 int64_t tot = 0;  // the row's integer dot product, |tot| < K * 2^38
 #pragma unroll
                 for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
-                v[e] = row < w.rows ? dn::round_to_i32((dn::i128)tot * (dn::i128)w.row_scale[row], 24) : 0;
+                const int64_t sc = row < w.rows ? w.row_scale[row] : 0;
+                const uint64_t at = tot < 0 ? 0 - (uint64_t)tot : (uint64_t)tot;
+                const uint64_t as = sc < 0 ? 0 - (uint64_t)sc : (uint64_t)sc;
+                fits &= (128 - __clzll(at) - __clzll(as)) <= 63;  // |tot * sc| < 2^63
+                v[e] = dn::clamp_i64_to_i32(dn::rshift_rte((int64_t)((uint64_t)tot * (uint64_t)sc), 24));
+            }
+            if (!__all(fits)) {
+#pragma unroll
+                for (int e = 0; e < 16; e++) {
+                    const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4),
+                                   row = rt0 * 32 + rl;
+                    int64_t tot = 0;
+#pragma unroll
+                    for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
+                    v[e] = row < w.rows ? dn::round_to_i32((dn::i128)tot * (dn::i128)w.row_scale[row], 24) : 0;
+                }
             }
             if (pairs) {
                 // Rows e and e + 1 (e even) are a gate/up pair in this lane:
