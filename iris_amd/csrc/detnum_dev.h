@@ -378,11 +378,9 @@ __device__ inline uint64_t exp_neg_q32(uint64_t a) {
 // the quotient, so its floor is off by at most one) corrected on the exact
 // remainder.
 __device__ __forceinline__ uint64_t floor_2p63_over(uint64_t d) {
-    uint64_t q = (uint64_t)(9223372036854775808.0 / (double)d);
+    const uint64_t q = (uint64_t)(9223372036854775808.0 / (double)d);
     const int64_t rem = (int64_t)(((uint64_t)1 << 63) - q * d);
-    if (rem < 0) q--;
-    else if ((uint64_t)rem >= d) q++;
-    return q;
+    return q - (uint64_t)(rem < 0) + (uint64_t)(rem >= 0 && (uint64_t)rem >= d);
 }
 
 // mistral.rs:59-77
