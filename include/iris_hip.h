@@ -80,6 +80,21 @@ uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* matrix, uint32_t tokens);
 int q8gpu_product_device_ws(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens,
                             int32_t* d_out, void* d_workspace, uint64_t workspace_bytes, void* stream);
 
+/* Bytes of each device's scratch array (below): 32 MiB. */
+#define IRIS_NOALLOC_SCRATCH_BYTES (32ull << 20)
+
+/* q8gpu_product_device_ws without any allocation: the work space is a
+ * file-scope device array of IRIS_NOALLOC_SCRATCH_BYTES per device, held
+ * until the process ends. No counterpart in the reference: it is for callers
+ * that cannot allocate (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Returns IRIS_E_SCRATCH (-6), and runs
+ * nothing, when q8gpu_workspace_bytes(matrix, tokens) exceeds the array.
+ * Every call on one device shares that device's array: calls that overlap on
+ * one device (other streams, other threads) race and must be serialised by
+ * the caller; calls in order on one stream are safe. */
+int q8gpu_product_device_noalloc(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens,
+                                 int32_t* d_out, void* stream);
+
 /* rows, cols and the device layout the upload chose: 0 = one scale per row
  * (every block of each row shares it), 1 = one f16 per block, 2 = one i64 per
  * block; bytes = device memory held. */

@@ -58,6 +58,35 @@ int f16_bits_of_q24(int64_t s) {
     return (int)(sign | ((uint32_t)(e + 1) << 10) | mant);
 }
 
+// The no-allocation product's work space: one array per device, holding the
+// digit planes and per-token digit counts of one multi-token product. In host
+// code `scratch` only names the symbol; its device address on each device
+// comes from hipGetSymbolAddress, resolved once per device (q8gpu_init for
+// the current device, else the entry point's first call there) and kept in
+// g_scratch_dev, which is all host code ever passes on.
+__device__ __align__(256) uint8_t scratch[IRIS_NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_lock;
+uint8_t* g_scratch_dev[MAX_DEVICES] = {};
+
+int scratch_for_current_device(uint8_t** out) {
+    int dev = 0;
+    hipError_t st = hipGetDevice(&dev);
+    if (st != hipSuccess) return (int)st;
+    if (dev < 0 || dev >= MAX_DEVICES) return IRIS_E_INVALID;
+    std::lock_guard<std::mutex> guard(g_scratch_lock);
+    if (!g_scratch_dev[dev]) {
+        void* p = nullptr;
+        st = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (st != hipSuccess) return (int)st;
+        if (!p) return IRIS_E_STATE;
+        g_scratch_dev[dev] = (uint8_t*)p;
+    }
+    *out = g_scratch_dev[dev];
+    return 0;
+}
+
 }  // namespace
 
 void iris_set_error_text(const char* text) { g_error_text = text; }
@@ -126,6 +155,7 @@ const char* q8gpu_error(int code) {
         case IRIS_E_NOMEM: return "host allocation failed";
         case IRIS_E_STATE: return "call made in the wrong state";
         case IRIS_E_RANGE: return "position or size past what the object was built for";
+        case IRIS_E_SCRATCH: return "work space needed exceeds the no-allocation scratch (IRIS_NOALLOC_SCRATCH_BYTES)";
         default: break;
     }
     if (code < 0) return g_error_text ? g_error_text : "unknown library error";
@@ -137,7 +167,10 @@ int q8gpu_init(void) {
     hipError_t st = hipMalloc(&probe, 1 << 20);
     if (st != hipSuccess) return (int)st;
     iris_gemv_prepare();
-    return (int)hipFree(probe);
+    st = hipFree(probe);
+    if (st != hipSuccess) return (int)st;
+    uint8_t* ws = nullptr;
+    return scratch_for_current_device(&ws);
 }
 
 void q8gpu_free(Q8GpuMatrix* m) {
@@ -247,6 +280,22 @@ int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t
         a.token_limbs = (int32_t*)((char*)d_workspace + planes_bytes(m->cols, tokens));
     }
     return iris_gemv_launch(a, (hipStream_t)stream);
+}
+
+// q8gpu_product_device_ws with the device's scratch array as the work space:
+// no allocation of any kind. The digit counts are reset per token and every
+// plane of the used region is written by the call itself before it is read,
+// so nothing carried over from an earlier call is used.
+int q8gpu_product_device_noalloc(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
+                                 void* stream) {
+    if (!m || (tokens && (!d_act || !d_out))) return IRIS_E_INVALID;
+    const uint64_t need = q8gpu_workspace_bytes(m, tokens);
+    if (need == 0) return q8gpu_product_device_ws(m, d_act, tokens, d_out, nullptr, 0, stream);
+    if (need > IRIS_NOALLOC_SCRATCH_BYTES) return IRIS_E_SCRATCH;
+    uint8_t* ws = nullptr;
+    const int rc = scratch_for_current_device(&ws);
+    if (rc != 0) return rc;
+    return q8gpu_product_device_ws(m, d_act, tokens, d_out, ws, IRIS_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int q8gpu_product(const Q8GpuMatrix* m, const int32_t* activations, uint32_t tokens, int32_t* out) {

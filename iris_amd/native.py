@@ -62,6 +62,7 @@ def _declare(L):
         "q8gpu_product_device": (C.c_int, [vp, vp, u32, vp, vp]),
         "q8gpu_workspace_bytes": (u64, [vp, u32]),
         "q8gpu_product_device_ws": (C.c_int, [vp, vp, u32, vp, vp, u64, vp]),
+        "q8gpu_product_device_noalloc": (C.c_int, [vp, vp, u32, vp, vp]),
         "q8gpu_matrix_info": (C.c_int, [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(C.c_int), C.POINTER(u64)]),
         "q8gpu_synchronize": (C.c_int, []),
         "iris_device_malloc": (C.c_int, [u64, pp]),
