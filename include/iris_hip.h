@@ -208,6 +208,15 @@ int iris_session_generate(IrisSession* session, const int32_t* prompt, uint32_t 
 int iris_session_layer_pass(IrisSession* session, const int32_t* ids, uint32_t count, int32_t* out_rows,
                             uint8_t* out_hashes);
 
+/* Copies a layer's cached keys and values of positions pos0..pos0+count to
+ * host memory: k_out and v_out get one row of kv_heads*head_dim int32 per
+ * position, the k and v of the reference's KeyRow
+ * (raster-stages/prefill-range/src/input.rs:185-189; emitted per layer by
+ * crates/inference/kernels/src/mistral/stage.rs:172-226). Waits for the
+ * session's work first. */
+int iris_session_read_kv(IrisSession* session, uint32_t layer, uint32_t pos0, uint32_t count, int32_t* k_out,
+                         int32_t* v_out);
+
 /* Times `steps` decode passes (graph replays) after the prompt pass and
  * reports milliseconds per decode token from HIP events on the session's
  * stream; the generated ids are written to out_tokens (nullable). */

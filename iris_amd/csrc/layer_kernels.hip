@@ -203,15 +203,15 @@ int attention_decode_launch(const AttnArgs& a, hipStream_t stream) {
 }
 
 // Dequantize one Q8_0 row (reference layout) into out[0..cols) (q8.rs:76-92),
-// optionally times a Q16.16 scale (model.rs:316-330).
+// times a Q16.16 scale (model.rs:316-330: gemma-dense's embedding scale, any
+// value including zero; mistral-dense passes 1.0, which mul_sat leaves exact).
 __device__ __forceinline__ void embed_row(const uint8_t* row, uint32_t cols, int32_t scale, int32_t* out,
                                           uint32_t tid, uint32_t nthreads) {
     for (uint32_t c = tid; c < cols; c += nthreads) {
         const uint8_t* blk = row + (size_t)(c / 32) * 34;
         const int64_t s = dn::scale_q24((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
         int32_t v = dn::round_to_i32((dn::i128)((int64_t)(int8_t)blk[2 + c % 32] * s), 8);
-        if (scale != 0) v = dn::mul_sat(v, scale);
-        out[c] = v;
+        out[c] = dn::mul_sat(v, scale);
     }
 }
 

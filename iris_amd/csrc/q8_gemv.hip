@@ -195,8 +195,7 @@ __global__ __launch_bounds__(SELECT_THREADS) void select_embed_kernel(const Gemv
         const uint8_t* blk = er + (size_t)(c / 32) * 34;
         const int64_t sc = dn::scale_q24((uint32_t)blk[0] | ((uint32_t)blk[1] << 8));
         int32_t e = dn::round_to_i32((dn::i128)((int64_t)(int8_t)blk[2 + c % 32] * sc), 8);
-        if (a.embed_scale != 0) e = dn::mul_sat(e, a.embed_scale);
-        a.x_next[c] = e;
+        a.x_next[c] = dn::mul_sat(e, a.embed_scale);
     }
     if (tid == 0) {
         const int32_t step = *a.d_step;

@@ -103,7 +103,7 @@ struct GemvArgs {
     int32_t* tokens_out;        // [steps]
     const uint8_t* embed_raw;   // Q8_0 rows, reference layout
     uint32_t embed_row_bytes, hidden;
-    int32_t embed_scale;        // 0 = unscaled
+    int32_t embed_scale;        // Q16.16 multiplier of the embedded row (1.0 for mistral-dense)
     int32_t* x_next;            // [hidden]
     int32_t* ids_next;          // nullable: the selected id is also stored here
     uint64_t* sel_partial;      // [tiles]: (index << 32) | (uint32)value of each tile's first maximum

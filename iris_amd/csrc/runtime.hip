@@ -49,6 +49,14 @@ int layer_of(const std::string& name, std::string* suffix) {
         if (rc_ != 0) return rc_;       \
     } while (0)
 
+// False when a block of raw Q8_0 rows has a non-finite f16 scale (exponent
+// 0x1f), which dequantize_row refuses (q8.rs:45-47, 76-92).
+bool q8_scales_finite(const uint8_t* raw, size_t blocks) {
+    for (size_t b = 0; b < blocks; b++)
+        if ((raw[b * 34 + 1] & 0x7c) == 0x7c) return false;
+    return true;
+}
+
 template <class T>
 hipError_t dev_alloc_copy(T** dst, const void* src, size_t bytes) {
     hipError_t st = hipMalloc((void**)dst, bytes ? bytes : 4);
@@ -220,6 +228,7 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
     }
     if (name == std::string(PREFIX) + "embed_tokens.weight") {
         if (width != 8 || rows != d.vocab || cols != d.hidden) return IRIS_E_INVALID;
+        if (!q8_scales_finite((const uint8_t*)data, bytes / 34)) return IRIS_E_SCALE;
         RT_CHECK(dev_alloc_copy(&m->embed_raw, data, bytes));
         m->embed_row_bytes = (uint32_t)(cols / 32 * 34);
         if (d.tied_head) {
@@ -246,6 +255,7 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
         const uint64_t lp = (uint64_t)d.layers * d.ple_width;
         if (name == std::string(PREFIX) + "embed_tokens_per_layer.weight") {
             if (width != 8 || rows != d.vocab || cols != lp) return IRIS_E_INVALID;
+            if (!q8_scales_finite((const uint8_t*)data, bytes / 34)) return IRIS_E_SCALE;
             RT_CHECK(dev_alloc_copy(&m->embed_ple, data, bytes));
             m->embed_ple_row_bytes = (uint32_t)(cols / 32 * 34);
             return 0;
@@ -984,6 +994,33 @@ int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, 
     for (auto& th : pool) th.join();
     RT_CHECK(hipStreamSynchronize(s->stream));
     return status;
+}
+
+// The K cache is transposed ([kv_rows][k_pos_stride]): the block of the
+// asked positions comes over as kv_rows strided runs and is transposed into
+// position rows on the host; V rows are already position rows.
+int iris_session_read_kv(IrisSession* s, uint32_t layer, uint32_t pos0, uint32_t count, int32_t* k_out,
+                         int32_t* v_out) {
+    if (!s || (count && (!k_out || !v_out))) return IRIS_E_INVALID;
+    const IrisModelDesc& d = s->model->d;
+    if (layer >= d.layers) return IRIS_E_INVALID;
+    if ((uint64_t)pos0 + count > s->max_positions) return IRIS_E_RANGE;
+    if (count == 0) return 0;
+    const size_t kvw = s->model->layers[layer].kv_rows;
+    std::vector<int32_t> kt;
+    try {
+        kt.resize(kvw * count);
+    } catch (...) {
+        return IRIS_E_NOMEM;
+    }
+    RT_CHECK(hipStreamSynchronize(s->stream));
+    RT_CHECK(hipMemcpy2D(kt.data(), (size_t)count * 4, s->k_cache[layer] + pos0, (size_t)s->k_pos_stride * 4,
+                         (size_t)count * 4, kvw, hipMemcpyDeviceToHost));
+    RT_CHECK(hipMemcpy(v_out, s->v_cache[layer] + (size_t)pos0 * kvw, (size_t)count * kvw * 4,
+                       hipMemcpyDeviceToHost));
+    for (size_t c = 0; c < kvw; c++)
+        for (size_t p = 0; p < count; p++) k_out[p * kvw + c] = kt[c * count + p];
+    return 0;
 }
 
 int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, double* ms) {

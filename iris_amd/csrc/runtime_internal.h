@@ -48,7 +48,7 @@ struct IrisModel {
     int32_t* final_norm = nullptr;
     int64_t* inv_freq = nullptr;
     int32_t head_softcap = 0;   // 0 = uncapped (mistral-dense)
-    int32_t embed_scale = 0;    // 0 = unscaled (mistral-dense)
+    int32_t embed_scale = 1 << 16;  // mul_sat of each embedded value; 1.0 (exact) for mistral-dense
     // gemma-dense only
     uint8_t* embed_ple = nullptr;        // embed_tokens_per_layer, reference Q8_0 rows
     uint32_t embed_ple_row_bytes = 0;

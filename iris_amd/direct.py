@@ -52,6 +52,7 @@ def _declare():
         "iris_session_layer_pass": (C.c_int, [vp, vp, u32, vp, vp]),
         "iris_session_time_decode": (C.c_int, [vp, vp, u32, u32, C.POINTER(C.c_double), C.POINTER(C.c_double), vp]),
         "iris_session_time_pass": (C.c_int, [vp, vp, u32, C.POINTER(C.c_double)]),
+        "iris_session_read_kv": (C.c_int, [vp, u32, u32, u32, vp, vp]),
         "iris_sha256_bytes": (C.c_int, [vp, u64, vp]),
     }
     for name, (res, args) in sig.items():
@@ -196,6 +197,17 @@ class Session:
                                                            C.byref(ms), C.byref(pre), toks.ctypes.data),
                      "time decode")
         return ms.value, pre.value, toks.tolist()
+
+    def read_kv(self, layer: int, pos0: int, count: int):
+        """A layer's cached (k, v) rows of positions pos0..pos0+count, each
+        [count, kv_heads*head_dim] int32 (the reference's KeyRow k and v)."""
+        m = self.dm.model
+        kvw = m.shape.num_key_value_heads * m.head_dim_at(layer)
+        k = np.empty((count, kvw), dtype=np.int32)
+        v = np.empty((count, kvw), dtype=np.int32)
+        native.check(native.lib().iris_session_read_kv(self._h, layer, pos0, count, k.ctypes.data, v.ctypes.data),
+                     "read kv")
+        return k, v
 
     def time_pass(self, ids) -> float:
         """Milliseconds of one pass of every layer over ``ids`` (HIP events)."""

@@ -24,6 +24,14 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 _lib = None
 
 
+def default_threads() -> int:
+    """Host threads for the oracle: the CPU count, capped by OMP_NUM_THREADS
+    when it is set (the share of the host a run is given)."""
+    n = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    return max(1, min(n, int(env))) if env.isdigit() and int(env) > 0 else n
+
+
 def build() -> str:
     subprocess.run(["make", "-s", "-C", HERE], check=True)
     return LIB_PATH
@@ -42,6 +50,7 @@ def lib():
 i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
 u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
 
 
 class MistralLayerC(C.Structure):
@@ -102,7 +111,10 @@ def _declare(L):
                                               i32p, i32p, C.c_int]),
         "orc_gemma_ple_prepare": (C.c_int, [i32p, sz, i32p, sz, i32, i32p, i64, u8p, sz, i32, i32, i32p]),
         "orc_head_logits": (C.c_int, [i32p, sz, i32p, i64, i32, u8p, sz, i32p, C.c_int]),
-        "orc_embedding_row": (C.c_int, [u8p, sz, i32, i32p]),
+        "orc_embedding_row": (C.c_int, [u8p, sz, C.c_int, i32, i32p]),
+        "orc_silu_many": (C.c_int, [i32p, sz, i32p, C.c_int]),
+        "orc_mistral_layer_rows": (C.c_int, [C.POINTER(MistralLayerC), i32p, sz, u32, i32p, i32p, u32p, sz, i32p,
+                                             C.c_int]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
@@ -132,22 +144,31 @@ def q8_dot_row(act, row) -> int:
     return out.value
 
 
-def linear_q8(inp, w, threads: int = os.cpu_count() or 1) -> np.ndarray:
+def linear_q8(inp, w, threads: int = 0) -> np.ndarray:
     """tokens x rows products of a Q8_0 matrix (raw bytes [rows, cols/32*34])."""
     inp = _c(np.atleast_2d(inp), np.int32)
     w = _c(w, np.uint8)
     tokens, cols = inp.shape
     rows = w.shape[0]
     out = np.empty((tokens, rows), dtype=np.int32)
-    _check(lib().orc_linear_q8(inp, tokens, cols, w, rows, out, threads), "linear_q8")
+    _check(lib().orc_linear_q8(inp, tokens, cols, w, rows, out, threads or default_threads()), "linear_q8")
     return out
 
 
-def linear_i32(inp, w, threads: int = os.cpu_count() or 1) -> np.ndarray:
+def linear_i32(inp, w, threads: int = 0) -> np.ndarray:
     inp = _c(np.atleast_2d(inp), np.int32)
     w = _c(w, np.int32)
     out = np.empty((inp.shape[0], w.shape[0]), dtype=np.int32)
-    _check(lib().orc_linear_i32(inp, inp.shape[0], inp.shape[1], w, w.shape[0], out, threads), "linear_i32")
+    _check(lib().orc_linear_i32(inp, inp.shape[0], inp.shape[1], w, w.shape[0], out, threads or default_threads()),
+           "linear_i32")
+    return out
+
+
+def silu_many(x, threads: int = 0) -> np.ndarray:
+    """mistral.rs:72-77 silu of every value."""
+    x = _c(x, np.int32).reshape(-1)
+    out = np.empty_like(x)
+    _check(lib().orc_silu_many(x, x.size, out, threads or default_threads()), "silu")
     return out
 
 
@@ -203,9 +224,9 @@ class OracleRun:
     """The reference's direct token loop over a model (iris_amd.model.Model
     duck type: family, shape, q8()/values()/layer_name()/... accessors)."""
 
-    def __init__(self, model, max_positions: int, threads: int = os.cpu_count() or 1):
+    def __init__(self, model, max_positions: int, threads: int = 0):
         self.m = model
-        self.threads = threads
+        self.threads = threads or default_threads()
         self.max_positions = max_positions
         self.keep = []  # numpy arrays the C structs point into
         s = model.shape
@@ -274,11 +295,12 @@ class OracleRun:
         m = self.m
         H = m.hidden
         table = m.q8(m.embedding_name())
-        scale = m.shape.embedding_scale if m.family == "gemma-dense" else 0
+        scaled = m.family == "gemma-dense"  # only gemma-dense scales its embeddings
+        scale = m.shape.embedding_scale if scaled else 0
         out = np.empty((len(ids), H), dtype=np.int32)
         for i, t in enumerate(ids):
             row = np.empty(H, dtype=np.int32)
-            _check(lib().orc_embedding_row(_c(table[int(t)], np.uint8), H, scale, row), "embedding")
+            _check(lib().orc_embedding_row(_c(table[int(t)], np.uint8), H, int(scaled), scale, row), "embedding")
             out[i] = row
         return out
 
@@ -314,6 +336,18 @@ class OracleRun:
                                                  self.k_cache[layer], self.v_cache[layer], self.k_cache[src],
                                                  self.v_cache[src], ple, out, self.threads),
                    f"gemma layer {layer}")
+        return out
+
+    def mistral_layer_rows(self, layer: int, x: np.ndarray, start: int, sel) -> np.ndarray:
+        """One mistral-dense layer over rows at positions start..start+len(x):
+        every row's keys and values into this run's caches, the layer output
+        only for the row indices in ``sel`` ([len(sel), hidden])."""
+        x = _c(x, np.int32)
+        sel = _c(sel, np.uint32)
+        out = np.empty((sel.size, x.shape[1]), dtype=np.int32)
+        _check(lib().orc_mistral_layer_rows(C.byref(self.layers[layer]), x, x.shape[0], start, self.k_cache[layer],
+                                            self.v_cache[layer], sel, sel.size, out, self.threads),
+               f"mistral layer {layer} rows")
         return out
 
     def pass_rows(self, ids, start: int, keep_layers: bool = False):

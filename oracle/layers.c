@@ -69,40 +69,49 @@ static void mistral_attention_context(const orc_mistral_layer* L, const int32_t*
     }
 }
 
-int orc_mistral_layer_forward(const orc_mistral_layer* L, const int32_t* x, size_t count, uint32_t start,
-                              int32_t* k_cache, int32_t* v_cache, int32_t* out, int threads) {
-    size_t H = L->hidden, F = L->ffn, hd = L->head_dim;
-    size_t qw = (size_t)L->heads * hd, kvw = (size_t)L->kv_heads * hd;
-    if (!H || !F || !L->heads || !L->kv_heads || !hd || L->heads % L->kv_heads || hd % 2) return ORC_EBAD;
-    if (count == 0) return 0;
-    if ((uint64_t)start + count > L->max_positions) return ORC_EBAD; /* layer.rs:116-123 */
-    int rc = 0;
-    int32_t* normed = malloc(count * H * 4);
-    int32_t* q = malloc(count * qw * 4);
-    int32_t* ctx = malloc(count * qw * 4);
-    int32_t* attended = malloc(count * H * 4);
-    int32_t* ffin = malloc(count * H * 4);
-    int32_t* gate = malloc(count * F * 4);
-    int32_t* up = malloc(count * F * 4);
-    if (!normed || !q || !ctx || !attended || !ffin || !gate || !up) { rc = ORC_ENOMEM; goto done; }
-    /* :144-148 */
+/* mistral/layer.rs:144-162: rms_norm(norm_attention) of every row, then the
+ * range's own keys and values into the caches at start.., k rotated at its
+ * absolute position (:163-185). */
+static int mistral_keys(const orc_mistral_layer* L, const int32_t* x, size_t count, uint32_t start,
+                        int32_t* normed, int32_t* k_cache, int32_t* v_cache, int threads) {
+    size_t H = L->hidden, hd = L->head_dim, kvw = (size_t)L->kv_heads * hd;
+    int rc;
     memcpy(normed, x, count * H * 4);
     for (size_t i = 0; i < count; i++) dn_rms_norm(normed + i * H, L->norm_attention, H, L->norm_eps);
-    /* :149-151 */
-    if ((rc = orc_linear_q8(normed, count, H, L->w_q, qw, q, threads))) goto done;
-    if ((rc = orc_linear_q8(normed, count, H, L->w_k, kvw, k_cache + (size_t)start * kvw, threads))) goto done;
-    if ((rc = orc_linear_q8(normed, count, H, L->w_v, kvw, v_cache + (size_t)start * kvw, threads))) goto done;
-    /* :163-185 rotate every head of q and k at the row's absolute position */
+    if ((rc = orc_linear_q8(normed, count, H, L->w_k, kvw, k_cache + (size_t)start * kvw, threads))) return rc;
+    if ((rc = orc_linear_q8(normed, count, H, L->w_v, kvw, v_cache + (size_t)start * kvw, threads))) return rc;
     for (size_t i = 0; i < count; i++) {
-        for (size_t h = 0; h < L->heads; h++)
-            dn_rotate_consecutive_pairs(q + i * qw + h * hd, hd, L->inv_freq, hd / 2, start + (uint32_t)i);
         int32_t* kr = k_cache + ((size_t)start + i) * kvw;
         for (size_t h = 0; h < L->kv_heads; h++)
             dn_rotate_consecutive_pairs(kr + h * hd, hd, L->inv_freq, hd / 2, start + (uint32_t)i);
     }
-    /* :229-236 attention per row over positions 0..=row */
+    return 0;
+}
+
+/* The rest of mistral/layer.rs:149-267 for n rows whose inputs are x (and
+ * their normed copies), at absolute positions pos[i], over caches that hold
+ * every key up to each row's position: q (rotated), attention (:229-236), W_o
+ * + x (:237-242), rms_norm(norm_feed_forward), mul(silu(gate), up), W_down +
+ * attended (:243-267). */
+static int mistral_rows(const orc_mistral_layer* L, const int32_t* x, const int32_t* normed, const uint32_t* pos,
+                        size_t n, const int32_t* k_cache, const int32_t* v_cache, int32_t* out, int threads) {
+    size_t H = L->hidden, F = L->ffn, hd = L->head_dim;
+    size_t qw = (size_t)L->heads * hd;
+    int rc = 0;
+    int32_t* q = malloc(n * qw * 4);
+    int32_t* ctx = malloc(n * qw * 4);
+    int32_t* attended = malloc(n * H * 4);
+    int32_t* ffin = malloc(n * H * 4);
+    int32_t* gate = malloc(n * F * 4);
+    int32_t* up = malloc(n * F * 4);
+    if (!q || !ctx || !attended || !ffin || !gate || !up) { rc = ORC_ENOMEM; goto done; }
+    if ((rc = orc_linear_q8(normed, n, H, L->w_q, qw, q, threads))) goto done;
+    for (size_t i = 0; i < n; i++)
+        for (size_t h = 0; h < L->heads; h++)
+            dn_rotate_consecutive_pairs(q + i * qw + h * hd, hd, L->inv_freq, hd / 2, pos[i]);
     {
-        size_t end = (size_t)start + count;
+        size_t end = 0;
+        for (size_t i = 0; i < n; i++) end = pos[i] + 1 > end ? pos[i] + 1 : end;
         int rc2 = 0;
 #pragma omp parallel num_threads(threads > 0 ? threads : 1) reduction(| : rc2)
         {
@@ -112,29 +121,73 @@ int orc_mistral_layer_forward(const orc_mistral_layer* L, const int32_t* x, size
             if (!logits || !scratch || !weights) rc2 = 1;
             else {
 #pragma omp for schedule(dynamic)
-                for (long long i = 0; i < (long long)count; i++)
-                    mistral_attention_context(L, q + i * qw, start + (size_t)i, k_cache, v_cache,
-                                              ctx + i * qw, logits, scratch, weights);
+                for (long long i = 0; i < (long long)n; i++)
+                    mistral_attention_context(L, q + i * qw, pos[i], k_cache, v_cache, ctx + i * qw, logits, scratch,
+                                              weights);
             }
             free(logits); free(scratch); free(weights);
         }
         if (rc2) { rc = ORC_ENOMEM; goto done; }
     }
-    /* :237-242 W_o, then + x */
-    if ((rc = orc_linear_q8(ctx, count, qw, L->w_o, H, attended, threads))) goto done;
-    for (size_t i = 0; i < count * H; i++) attended[i] = dn_add_sat(attended[i], x[i]);
-    /* :243-250 */
-    memcpy(ffin, attended, count * H * 4);
-    for (size_t i = 0; i < count; i++) dn_rms_norm(ffin + i * H, L->norm_feed_forward, H, L->norm_eps);
-    if ((rc = orc_linear_q8(ffin, count, H, L->w_gate, F, gate, threads))) goto done;
-    if ((rc = orc_linear_q8(ffin, count, H, L->w_up, F, up, threads))) goto done;
-    /* :251-258 mul(silu(gate), up) */
-    for (size_t i = 0; i < count * F; i++) gate[i] = dn_mul_sat(dn_silu(gate[i]), up[i]);
-    /* :259-267 W_down, then + attended */
-    if ((rc = orc_linear_q8(gate, count, F, L->w_down, H, out, threads))) goto done;
-    for (size_t i = 0; i < count * H; i++) out[i] = dn_add_sat(out[i], attended[i]);
+    if ((rc = orc_linear_q8(ctx, n, qw, L->w_o, H, attended, threads))) goto done;
+    for (size_t i = 0; i < n * H; i++) attended[i] = dn_add_sat(attended[i], x[i]);
+    memcpy(ffin, attended, n * H * 4);
+    for (size_t i = 0; i < n; i++) dn_rms_norm(ffin + i * H, L->norm_feed_forward, H, L->norm_eps);
+    if ((rc = orc_linear_q8(ffin, n, H, L->w_gate, F, gate, threads))) goto done;
+    if ((rc = orc_linear_q8(ffin, n, H, L->w_up, F, up, threads))) goto done;
+    for (size_t i = 0; i < n * F; i++) gate[i] = dn_mul_sat(dn_silu(gate[i]), up[i]);
+    if ((rc = orc_linear_q8(gate, n, F, L->w_down, H, out, threads))) goto done;
+    for (size_t i = 0; i < n * H; i++) out[i] = dn_add_sat(out[i], attended[i]);
 done:
-    free(normed); free(q); free(ctx); free(attended); free(ffin); free(gate); free(up);
+    free(q); free(ctx); free(attended); free(ffin); free(gate); free(up);
+    return rc;
+}
+
+static int mistral_check(const orc_mistral_layer* L) {
+    if (!L->hidden || !L->ffn || !L->heads || !L->kv_heads || !L->head_dim || L->heads % L->kv_heads ||
+        L->head_dim % 2)
+        return ORC_EBAD;
+    return 0;
+}
+
+int orc_mistral_layer_forward(const orc_mistral_layer* L, const int32_t* x, size_t count, uint32_t start,
+                              int32_t* k_cache, int32_t* v_cache, int32_t* out, int threads) {
+    if (mistral_check(L)) return ORC_EBAD;
+    if (count == 0) return 0;
+    if ((uint64_t)start + count > L->max_positions) return ORC_EBAD; /* layer.rs:116-123 */
+    int32_t* normed = malloc(count * L->hidden * 4);
+    uint32_t* pos = malloc(count * 4);
+    int rc = normed && pos ? 0 : ORC_ENOMEM;
+    for (size_t i = 0; rc == 0 && i < count; i++) pos[i] = start + (uint32_t)i;
+    if (rc == 0) rc = mistral_keys(L, x, count, start, normed, k_cache, v_cache, threads);
+    if (rc == 0) rc = mistral_rows(L, x, normed, pos, count, k_cache, v_cache, out, threads);
+    free(normed);
+    free(pos);
+    return rc;
+}
+
+int orc_mistral_layer_rows(const orc_mistral_layer* L, const int32_t* x, size_t count, uint32_t start,
+                           int32_t* k_cache, int32_t* v_cache, const uint32_t* sel, size_t n_sel, int32_t* out,
+                           int threads) {
+    if (mistral_check(L)) return ORC_EBAD;
+    if (count == 0 || n_sel == 0) return 0;
+    if ((uint64_t)start + count > L->max_positions) return ORC_EBAD;
+    size_t H = L->hidden;
+    for (size_t i = 0; i < n_sel; i++)
+        if (sel[i] >= count) return ORC_EBAD;
+    int32_t* normed = malloc(count * H * 4);
+    int32_t* xs = malloc(n_sel * H * 4);
+    int32_t* ns = malloc(n_sel * H * 4);
+    uint32_t* pos = malloc(n_sel * 4);
+    int rc = normed && xs && ns && pos ? 0 : ORC_ENOMEM;
+    if (rc == 0) rc = mistral_keys(L, x, count, start, normed, k_cache, v_cache, threads);
+    for (size_t i = 0; rc == 0 && i < n_sel; i++) {
+        memcpy(xs + i * H, x + (size_t)sel[i] * H, H * 4);
+        memcpy(ns + i * H, normed + (size_t)sel[i] * H, H * 4);
+        pos[i] = start + sel[i];
+    }
+    if (rc == 0) rc = mistral_rows(L, xs, ns, pos, n_sel, k_cache, v_cache, out, threads);
+    free(normed); free(xs); free(ns); free(pos);
     return rc;
 }
 
@@ -306,9 +359,15 @@ int orc_head_logits(const int32_t* last_row, size_t hidden, const int32_t* norm,
     return rc;
 }
 
-int orc_embedding_row(const uint8_t* emb_row, size_t hidden, int32_t embedding_scale, int32_t* out) {
+int orc_embedding_row(const uint8_t* emb_row, size_t hidden, int scaled, int32_t embedding_scale, int32_t* out) {
     if (dn_q8_dequantize_row(emb_row, hidden, out)) return ORC_ESCALE;
-    if (embedding_scale != 0)
+    if (scaled)
         for (size_t c = 0; c < hidden; c++) out[c] = dn_mul_sat(out[c], embedding_scale);
+    return 0;
+}
+
+int orc_silu_many(const int32_t* x, size_t n, int32_t* out, int threads) {
+#pragma omp parallel for schedule(static) num_threads(threads > 0 ? threads : 1)
+    for (long long i = 0; i < (long long)n; i++) out[i] = dn_silu(x[i]);
     return 0;
 }

@@ -49,6 +49,15 @@ typedef struct {
 int orc_mistral_layer_forward(const orc_mistral_layer* L, const int32_t* x, size_t count, uint32_t start,
                               int32_t* k_cache, int32_t* v_cache, int32_t* out, int threads);
 
+/* orc_mistral_layer_forward for the rows listed in sel (indices into the
+ * range, each < count): every row's keys and values go to the caches, as the
+ * full forward writes them, but q, attention, W_o and the feed-forward block
+ * run only for the listed rows; out is [n_sel][hidden], each row equal to the
+ * full forward's row of that index. */
+int orc_mistral_layer_rows(const orc_mistral_layer* L, const int32_t* x, size_t count, uint32_t start,
+                           int32_t* k_cache, int32_t* v_cache, const uint32_t* sel, size_t n_sel, int32_t* out,
+                           int threads);
+
 /* raster-stages/prefill-range/src/input.rs:91-190 LayerParams + TransformerLayer */
 typedef struct {
     uint32_t hidden, ffn, heads, kv_heads, head_dim, ple_width;
@@ -87,8 +96,12 @@ int orc_gemma_ple_prepare(const int32_t* embedded_row, size_t hidden, const int3
 int orc_head_logits(const int32_t* last_row, size_t hidden, const int32_t* norm, int64_t eps,
                     int32_t softcap, const uint8_t* head, size_t vocab, int32_t* logits, int threads);
 
-/* crates/inference/direct/src/model.rs:316-330 scaled_embedding_row
- * (embedding_scale 0 = unscaled, the mistral-dense case). */
-int orc_embedding_row(const uint8_t* emb_row, size_t hidden, int32_t embedding_scale, int32_t* out);
+/* crates/inference/direct/src/model.rs:316-330 scaled_embedding_row: the
+ * dequantized row, then mul_sat by embedding_scale when `scaled` (gemma-dense
+ * only; a zero scale gives a zero row). */
+int orc_embedding_row(const uint8_t* emb_row, size_t hidden, int scaled, int32_t embedding_scale, int32_t* out);
+
+/* mistral.rs:72-77 silu of n values (out[i] = silu(x[i])). */
+int orc_silu_many(const int32_t* x, size_t n, int32_t* out, int threads);
 
 #endif

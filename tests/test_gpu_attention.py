@@ -154,3 +154,23 @@ def test_long_context_decode_matches_oracle(family):
     assert np.array_equal(got.logits, np.stack(want_logits))
     s.free()
     dm.free()
+
+
+@pytest.mark.timeout(600)
+def test_silu_every_input():
+    # All 2^32 Q16.16 inputs, in chunks of 2^25: the device silu (the SwiGLU
+    # gate of the product epilogues) against the oracle's silu (mistral.rs:59-77).
+    chunk = 1 << 25
+    dx = native.DeviceBuffer(4 * chunk)
+    dout = native.DeviceBuffer(4 * chunk)
+    bad = 0
+    for c in range((1 << 32) // chunk):
+        x = (np.arange(chunk, dtype=np.int64) + (c * chunk - (1 << 31))).astype(np.int32)
+        native.check(native.lib().iris_memcpy_h2d(dx.ptr, x.ctypes.data, x.nbytes), "copy")
+        native.check(native.lib().iris_silu_device(dx.ptr, chunk, dout.ptr), "silu")
+        got = dout.to_array(np.int32, (chunk,))
+        want = cpu.silu_many(x)
+        bad += int(np.count_nonzero(got != want))
+        if c % 32 == 31:
+            print(f"silu: {(c + 1) * chunk} inputs checked, {bad} differ", flush=True)
+    assert bad == 0

@@ -148,3 +148,69 @@ def test_gemma_2b_shape_generation_matches_oracle():
     want_tokens, want_logits = _oracle_generate(m, prompt, 3, 64)
     assert got.token_ids == want_tokens
     assert np.array_equal(got.logits, np.stack(want_logits))
+
+
+# ---------------------------------------------------------------- selection and embedding edge cases
+
+@pytest.mark.parametrize("per_row_scale", [True, False])
+def test_tied_maxima_select_the_first_id(per_row_scale):
+    # generation.rs:25-33, 63-64: the first maximum in id order wins. The head
+    # holds one row w at ids 700 and 701 (one 16-row tile), 9000, 17000 and
+    # 31000 (other tiles, other selection waves, the selection's second round
+    # of tiles), its negation at 1300, 1301 and 20000, and zero rows
+    # elsewhere: every step's maximum is shared by several ids.
+    m = synth.mistral_model(256, 2, 4, 2, 64, 512, 32000, seed=23, per_row_scale=per_row_scale)
+    head = m.tensors["model.language_model.lm_head.weight"]
+    w = head[5].copy()
+    blocks = w.copy().reshape(-1, 34)
+    blocks[:, 2:] = (-(blocks[:, 2:].view(np.int8))).view(np.uint8)  # weights are in [-127, 127]
+    new = np.zeros_like(head)
+    for i in (700, 701, 9000, 17000, 31000):
+        new[i] = w
+    for i in (1300, 1301, 20000):
+        new[i] = blocks.reshape(-1)
+    m.tensors["model.language_model.lm_head.weight"] = new
+    prompt = synth.token_ids(24, 6, m.vocab)
+    dm = DeviceModel(m)
+    s = Session(dm, 64, 8)
+    got = s.generate(prompt, 12, keep_logits=True)
+    want_tokens, want_logits = _oracle_generate(m, prompt, 12, 64)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+    for logits in got.logits:
+        assert np.count_nonzero(logits == logits.max()) >= 2
+    assert set(got.token_ids) <= {0, 700, 1300}
+
+
+def test_gemma_embedding_scale_zero():
+    # model.rs:316-330 multiplies gemma-dense embeddings by their scale even
+    # when it is zero: every embedded row is zero.
+    import dataclasses
+    m = synth.tiny_gemma()
+    m.shape = dataclasses.replace(m.shape, embedding_scale=0)
+    prompt = synth.token_ids(25, 5, m.vocab)
+    dm = DeviceModel(m)
+    s = Session(dm, 32, 8)
+    got = s.generate(prompt, 4, keep_logits=True)
+    want_tokens, want_logits = _oracle_generate(m, prompt, 4, 32)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+
+
+@pytest.mark.parametrize("family,name", [("mistral-dense", "embed_tokens.weight"),
+                                         ("gemma-dense", "embed_tokens_per_layer.weight")])
+def test_non_finite_embedding_scale_is_refused(family, name):
+    # q8.rs:45-47: a Q8_0 scale with exponent 0x1f is not finite; the
+    # embedding tables (read by row, not uploaded as matrices: an untied
+    # mistral-dense embedding, the gemma-dense per-layer one) are refused at
+    # upload, as the matrices are.
+    if family == "mistral-dense":
+        m = synth.mistral_model(128, 1, 4, 2, 32, 256, 512, seed=26)
+    else:
+        m = synth.tiny_gemma()
+    t = m.tensors["model.language_model." + name].copy()
+    t[3, 0], t[3, 1] = 0x00, 0x7C  # +inf
+    m.tensors["model.language_model." + name] = t
+    with pytest.raises(native.IrisError) as e:
+        DeviceModel(m)
+    assert e.value.code == -2

@@ -174,6 +174,19 @@ def test_mfma_product_with_workspace(tokens, rows, cols):
         assert np.array_equal(dout.to_array(np.int32, (tokens, rows)), cpu.linear_q8(x, raw))
 
 
+def product_ws(m, x):
+    """q8gpu_product_device_ws with its work space: every output of x's tokens."""
+    L = native.lib()
+    tokens = x.shape[0]
+    ws_bytes = L.q8gpu_workspace_bytes(m.handle, tokens)
+    dx = native.DeviceBuffer.from_array(x)
+    dout = native.DeviceBuffer(tokens * m.rows * 4)
+    ws = native.DeviceBuffer(ws_bytes)
+    native.check(L.q8gpu_product_device_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, None), "product")
+    native.check(L.q8gpu_synchronize(), "sync")
+    return dout.to_array(np.int32, (tokens, m.rows))
+
+
 def grouped_activations(rng, tokens, cols):
     """Token group g (128 tokens each) needs exactly 1, 2, 3, 4, 5 digits for
     g = 0..4: magnitudes of 8, 15, 23 and 31 bits, then the full range with
@@ -210,3 +223,25 @@ def test_mfma_product_digit_paths(tokens, rows, cols):
     native.check(L.q8gpu_product_device_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, None), "product")
     native.check(L.q8gpu_synchronize(), "sync")
     assert np.array_equal(dout.to_array(np.int32, (tokens, rows)), cpu.linear_q8(x, raw))
+
+
+def test_mfma_product_wide_row_scales():
+    # Row-scale matrices whose Q.24 scales reach f16 exponent 30 (about 2^40),
+    # both signs, against full-range activations with every magnitude from 8
+    # to 32 bits: the MFMA epilogue's 64-bit rounding path, its bit-length
+    # test near 2^63 and its 128-bit redo all run; every output is compared.
+    rng = np.random.default_rng(31)
+    rows, cols, tokens = 512, 1024, 96
+    nb = cols // 32
+    exponent = np.concatenate([rng.integers(1, 12, 128), rng.integers(12, 22, 128), rng.integers(22, 31, 256)])
+    bits = ((rng.integers(0, 2, rows) << 15) | (exponent << 10) | rng.integers(0, 1024, rows)).astype(np.int64)
+    raw = np.empty((rows, nb, 34), np.uint8)
+    raw[:, :, 0] = (bits & 0xFF)[:, None]
+    raw[:, :, 1] = (bits >> 8)[:, None]
+    raw[:, :, 2:] = rng.integers(0, 256, (rows, nb, 32))
+    raw = raw.reshape(rows, -1)
+    m = Q8Matrix.from_bytes(raw, rows, cols)
+    assert m.info()["scale_mode"] == "row"
+    x = np.concatenate([rand_activations(rng, 1, cols, int(b)) for b in np.linspace(8, 32, tokens).astype(int)])
+    got = product_ws(m, x)
+    assert np.array_equal(got, cpu.linear_q8(x, raw))

@@ -236,3 +236,41 @@ def test_batched_prefill_equals_chunked_decode(family):
         assert (got == layers_full[layer]).all()
         assert (chunked.k_cache[layer][:5] == full.k_cache[layer][:5]).all()
         assert (chunked.v_cache[layer][:5] == full.v_cache[layer][:5]).all()
+
+
+def test_sampled_rows_equal_the_full_layer():
+    # orc_mistral_layer_rows (every row's keys, the listed rows' outputs)
+    # against the full forward, at position 0 and after carried keys.
+    m = synth.mistral_model(128, 2, 4, 2, 32, 256, 512, seed=13)
+    ids = list(synth.token_ids(14, 40, 512))
+    full = cpu.OracleRun(m, 64)
+    _, layers = full.pass_rows(ids, 0, keep_layers=True)
+    _, layers_after = full.pass_rows(ids[:9], 40, keep_layers=True)
+    sel = [0, 1, 17, 31, 39]
+    part = cpu.OracleRun(m, 64)
+    x = part.embed(ids)
+    for layer in range(m.num_layers):
+        out = part.mistral_layer_rows(layer, x, 0, sel)
+        assert (out == layers[layer][sel]).all()
+        assert (part.k_cache[layer][:40] == full.k_cache[layer][:40]).all()
+        assert (part.v_cache[layer][:40] == full.v_cache[layer][:40]).all()
+        x = layers[layer]
+    x = part.embed(ids[:9])
+    for layer in range(m.num_layers):
+        out = part.mistral_layer_rows(layer, x, 40, [0, 4, 8])
+        assert (out == layers_after[layer][[0, 4, 8]]).all()
+        assert (part.k_cache[layer][:49] == full.k_cache[layer][:49]).all()
+        x = layers_after[layer]
+
+
+def test_gemma_embedding_scale_zero_gives_zero_rows():
+    # model.rs:316-330: gemma-dense multiplies every embedded value by its
+    # scale, zero included; mistral-dense leaves the row as dequantized.
+    raw = synth.q8_matrix(synth.tensor_seed(15, 1), 4, 64, 0x3C00, False)
+    out = np.empty(64, dtype=np.int32)
+    assert cpu.lib().orc_embedding_row(raw[1], 64, 1, 0, out) == 0
+    assert not out.any()
+    assert cpu.lib().orc_embedding_row(raw[1], 64, 0, 0, out) == 0
+    want = np.empty(64, dtype=np.int32)
+    assert cpu.lib().dn_q8_dequantize_row(raw[1], 64, want) == 0
+    assert (out == want).all() and want.any()
