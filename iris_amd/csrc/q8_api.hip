@@ -12,28 +12,43 @@ namespace {
 
 thread_local const char* g_error_text = nullptr;
 
-// Device buffers for q8gpu_product's host round trip, grown as needed. Calls
-// are serialised by g_product_lock, as the reference's global device lock
+// q8gpu_product's host round trip runs in one device arena, carved per call
+// into the activations, the outputs and the MFMA work space (each region
+// 256-byte aligned). The arena only grows, to the next power of two of what
+// a call needs, so a run of similar products allocates once. Calls are
+// serialised by the arena's lock, as the reference's global device lock
 // serialises its products (gpu.rs:113-116).
-std::mutex g_product_lock;
-int32_t* g_scratch_act = nullptr;
-int32_t* g_scratch_out = nullptr;
-int32_t* g_scratch_ws = nullptr;  // the MFMA product's digit planes
-size_t g_scratch_act_bytes = 0, g_scratch_out_bytes = 0, g_scratch_ws_bytes = 0;
+struct RoundTripArena {
+    std::mutex lock;
+    uint8_t* base = nullptr;
+    uint64_t capacity = 0;
+
+    static uint64_t aligned(uint64_t bytes) { return (bytes + 255) & ~uint64_t(255); }
+
+    // Points act/out/ws at regions of the asked sizes (ws null when 0).
+    hipError_t carve(uint64_t act, uint64_t out, uint64_t ws, int32_t** a, int32_t** o, void** w) {
+        const uint64_t need = aligned(act) + aligned(out) + aligned(ws);
+        if (need > capacity) {
+            uint64_t grown = 1ull << 20;
+            while (grown < need) grown <<= 1;
+            if (base) hipFree(base);
+            base = nullptr;
+            capacity = 0;
+            const hipError_t st = hipMalloc((void**)&base, grown);
+            if (st != hipSuccess) return st;
+            capacity = grown;
+        }
+        *a = (int32_t*)base;
+        *o = (int32_t*)(base + aligned(act));
+        *w = ws ? (void*)(base + aligned(act) + aligned(out)) : nullptr;
+        return hipSuccess;
+    }
+};
+RoundTripArena g_round_trip;
 
 // Work space of a multi-token product: 5 digit planes of the activations
 // (256-byte aligned), then one digit count and one norm scale per token.
 uint64_t planes_bytes(uint32_t cols, uint32_t tokens) { return gemm_planes_bytes(cols, tokens); }
-
-hipError_t reserve(int32_t** buf, size_t* cap, size_t bytes) {
-    if (bytes <= *cap) return hipSuccess;
-    hipFree(*buf);
-    *buf = nullptr;
-    *cap = 0;
-    hipError_t st = hipMalloc((void**)buf, bytes);
-    if (st == hipSuccess) *cap = bytes;
-    return st;
-}
 
 Q8GpuMatrix* alloc_matrix(uint32_t rows, uint32_t cols) {
     Q8GpuMatrix* m = (Q8GpuMatrix*)std::calloc(1, sizeof(Q8GpuMatrix));
@@ -301,19 +316,18 @@ int q8gpu_product_device_noalloc(const Q8GpuMatrix* m, const int32_t* d_act, uin
 int q8gpu_product(const Q8GpuMatrix* m, const int32_t* activations, uint32_t tokens, int32_t* out) {
     if (!m || (tokens && (!activations || !out))) return IRIS_E_INVALID;
     if (tokens == 0) return 0;
-    std::lock_guard<std::mutex> guard(g_product_lock);
+    std::lock_guard<std::mutex> guard(g_round_trip.lock);
     const size_t act_bytes = (size_t)tokens * m->cols * sizeof(int32_t);
     const size_t out_bytes = (size_t)tokens * m->rows * sizeof(int32_t);
     const size_t ws_bytes = q8gpu_workspace_bytes(m, tokens);
-    hipError_t st = reserve(&g_scratch_act, &g_scratch_act_bytes, act_bytes);
-    if (st == hipSuccess) st = reserve(&g_scratch_out, &g_scratch_out_bytes, out_bytes);
-    if (st == hipSuccess && ws_bytes) st = reserve(&g_scratch_ws, &g_scratch_ws_bytes, ws_bytes);
-    if (st == hipSuccess) st = hipMemcpy(g_scratch_act, activations, act_bytes, hipMemcpyHostToDevice);
+    int32_t *d_act = nullptr, *d_out = nullptr;
+    void* d_ws = nullptr;
+    hipError_t st = g_round_trip.carve(act_bytes, out_bytes, ws_bytes, &d_act, &d_out, &d_ws);
+    if (st == hipSuccess) st = hipMemcpy(d_act, activations, act_bytes, hipMemcpyHostToDevice);
     if (st != hipSuccess) return (int)st;
-    int rc = q8gpu_product_device_ws(m, g_scratch_act, tokens, g_scratch_out, ws_bytes ? g_scratch_ws : nullptr,
-                                     ws_bytes, nullptr);
+    int rc = q8gpu_product_device_ws(m, d_act, tokens, d_out, d_ws, ws_bytes, nullptr);
     if (rc != 0) return rc;
-    st = hipMemcpy(out, g_scratch_out, out_bytes, hipMemcpyDeviceToHost);
+    st = hipMemcpy(out, d_out, out_bytes, hipMemcpyDeviceToHost);
     return (int)st;
 }
 
