@@ -208,6 +208,41 @@ int iris_session_generate(IrisSession* session, const int32_t* prompt, uint32_t 
 int iris_session_layer_pass(IrisSession* session, const int32_t* ids, uint32_t count, int32_t* out_rows,
                             uint8_t* out_hashes);
 
+/* The same chain pass over one range of a longer text: `count` rows at
+ * positions start_position.. attending over the keys the session's caches
+ * already hold for the positions before it (an earlier range's pass on this
+ * session, or keys carried in by iris_session_write_kv), as the range stages
+ * do (crates/inference/kernels/src/mistral/stage.rs:172-226,
+ * crates/inference/kernels/src/prefill_range.rs:82-172). Each layer's own
+ * keys stay in its cache for the next range (iris_session_read_kv returns
+ * them). Returns IRIS_E_STATE when a cache lacks a position the range needs
+ * (every one before start_position; for a sliding layer those in the first
+ * row's window), the reference's cache-coverage refusal
+ * (raster-stages/layer-mistral/src/lib.rs:889-940,
+ * raster-stages/prefill-range/src/lib.rs:1237-1290). A range at position 0
+ * starts the caches afresh. */
+int iris_session_layer_range(IrisSession* session, const int32_t* ids, uint32_t count, uint32_t start_position,
+                             int32_t* out_rows, uint8_t* out_hashes);
+
+/* One layer's stage over one range (run_layer_stage,
+ * crates/inference/kernels/src/mistral/stage.rs:172-226; gemma-dense
+ * run_prefill_range_direct, crates/inference/kernels/src/prefill_range.rs:82-172):
+ * in_rows (count x hidden, the layer below's output rows) at positions
+ * start_position.. over the layer's cached keys; out_rows gets the layer's
+ * rows and the rows' own keys join the layer's cache. gemma-dense also takes
+ * the layer's PLE rows (count x ple_width, the reference's PleRow values);
+ * mistral-dense passes null. Same coverage refusal as
+ * iris_session_layer_range, for this layer only. Synchronous. */
+int iris_session_layer_stage(IrisSession* session, uint32_t layer, const int32_t* in_rows, uint32_t count,
+                             uint32_t start_position, const int32_t* ple_rows, int32_t* out_rows);
+
+/* Writes carried keys into a layer's cache: positions pos0..pos0+count, one
+ * row of kv_heads*head_dim int32 of k and of v per position (the k and v of
+ * the reference's KeyRow, raster-stages/prefill-range/src/input.rs:185-189,
+ * that a range inherits as prior_kv). Waits for the session's work first. */
+int iris_session_write_kv(IrisSession* session, uint32_t layer, uint32_t pos0, uint32_t count, const int32_t* k,
+                          const int32_t* v);
+
 /* Copies a layer's cached keys and values of positions pos0..pos0+count to
  * host memory: k_out and v_out get one row of kv_heads*head_dim int32 per
  * position, the k and v of the reference's KeyRow

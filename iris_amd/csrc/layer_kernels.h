@@ -64,6 +64,8 @@ int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys,
 // plane space for `tokens` rows and `max_keys` keys.
 bool iris_attention_prefill_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys);
 int iris_attention_prefill_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
+// *d_pos = pos and *d_step = step, in stream order.
+int iris_set_counters_launch(int32_t* d_pos, int32_t pos, int32_t* d_step, int32_t step, hipStream_t stream);
 int iris_embed_rows_launch(const int32_t* d_ids, uint32_t count, const uint8_t* embed_raw, uint32_t row_bytes,
                            uint32_t hidden, int32_t scale, int32_t* out, hipStream_t stream);
 

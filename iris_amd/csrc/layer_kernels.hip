@@ -239,7 +239,20 @@ __global__ __launch_bounds__(256) void silu_kernel(const int32_t* x, uint32_t n,
     if (i < n) out[i] = dn::silu(x[i]);
 }
 
+// The pass position and the selection step of a session, set on its stream.
+__global__ void set_counters_kernel(int32_t* d_pos, int32_t pos, int32_t* d_step, int32_t step) {
+    if (threadIdx.x == 0) {
+        *d_pos = pos;
+        *d_step = step;
+    }
+}
+
 }  // namespace
+
+int iris_set_counters_launch(int32_t* d_pos, int32_t pos, int32_t* d_step, int32_t step, hipStream_t stream) {
+    hipLaunchKernelGGL(set_counters_kernel, dim3(1), dim3(64), 0, stream, d_pos, pos, d_step, step);
+    return (int)hipGetLastError();
+}
 
 extern "C" int iris_silu_device(const int32_t* d_x, uint32_t n, int32_t* d_out) {
     if (n == 0) return 0;

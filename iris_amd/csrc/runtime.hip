@@ -415,23 +415,19 @@ static int checkpoint_layer(IrisSession* s, const CkptSink* sink, uint32_t l, ui
     return (int)hipEventRecord(sink->events[l], s->stream);
 }
 
-static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+// One mistral-dense layer over the session's rows in s->x (positions from
+// *d_pos; the rows' RoPE table already in rope_sc), its output back in s->x.
+// With `slots` (one row), the residual products leave per-tile sums of
+// squares for the norms after them; ssq_x_in says whether s->ssq_x already
+// holds those of the layer's input.
+static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, bool ssq_x_in) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     const uint32_t H = d.hidden;
     const uint32_t qw = d.heads * d.head_dim, kvw = d.kv_heads * d.head_dim;
-    hipStream_t st = s->stream;
-    // The rows' RoPE (sin, cos) pairs, shared by every layer (for a one-row
-    // pass after a selection, the selection kernel has formed them).
-    if (!(rows == 1 && s->rope_ready))
-        RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, st));
-    s->rope_ready = false;
-    // One row: the residual products leave per-tile sums of squares for the
-    // norms after them (hidden rows in 16-row tiles, within the slot count).
     const uint32_t h_tiles = (H + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
-    const bool slots = rows == 1 && h_tiles <= GEMV_SSQ_SLOTS;
-    s->ssq_x_valid = false;
-    for (uint32_t l = 0; l < d.layers; l++) {
+    hipStream_t st = s->stream;
+    {
         const LayerWeights& L = m->layers[l];
         GemvArgs g{};
         // 1. q|k|v = W_qkv rms_norm(x); RoPE; K/V into the cache.
@@ -454,7 +450,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         g.k_cache = s->k_cache[l];
         g.k_pos_stride = s->k_pos_stride;
         g.v_cache = s->v_cache[l];
-        if (slots && l > 0) {
+        if (slots && ssq_x_in) {
             g.ssq_in = s->ssq_x;
             g.ssq_n = h_tiles;
         }
@@ -526,6 +522,25 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         if (slots) g.ssq_out = s->ssq_x;
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
+    }
+    return 0;
+}
+
+static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    // The rows' RoPE (sin, cos) pairs, shared by every layer (for a one-row
+    // pass after a selection, the selection kernel has formed them).
+    if (!(rows == 1 && s->rope_ready))
+        RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, s->stream));
+    s->rope_ready = false;
+    // One row: sums of squares pass from each residual product to the norm
+    // after it (hidden rows in 16-row tiles, within the slot count).
+    const uint32_t h_tiles = (d.hidden + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
+    const bool slots = rows == 1 && h_tiles <= GEMV_SSQ_SLOTS;
+    s->ssq_x_valid = false;
+    for (uint32_t l = 0; l < d.layers; l++) {
+        RT_CHECK(mistral_layer(s, l, rows, slots, l > 0));
         RT_CHECK(checkpoint_layer(s, sink, l, rows));
     }
     s->ssq_x_valid = slots && d.layers > 0;
@@ -535,12 +550,13 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
 // One gemma-dense pass (crates/inference/kernels/src/prefill_range.rs:307-958
 // per layer, the PLE prepare of view_kernels.rs:59-99 first): eleven launches
 // per layer.
-static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+// The PLE inputs of every layer (view_kernels.rs:59-99) from the embedded
+// rows in s->x and their ids, into s->ple_rows [rows][layers * ple_width].
+static int gemma_ple(IrisSession* s, uint32_t rows) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     const uint32_t H = d.hidden, P = d.ple_width, LP = d.layers * d.ple_width;
     hipStream_t st = s->stream;
-    // PLE inputs of every layer from the embedded rows and their ids.
     I32GemvArgs ig{};
     ig.w = m->ple_model_proj;
     ig.rows = LP;
@@ -563,8 +579,18 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     pa.embedding_scale = d.ple_embedding_scale;
     pa.input_scale = d.ple_input_scale;
     pa.out = s->ple_rows;
-    RT_CHECK(iris_ple_prepare_launch(pa, d.layers, rows, st));
-    for (uint32_t l = 0; l < d.layers; l++) {
+    return iris_ple_prepare_launch(pa, d.layers, rows, st);
+}
+
+// One gemma-dense layer over the rows in s->x (positions from *d_pos), with
+// the layer's PLE inputs in s->ple_rows; the output back in s->x.
+static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    const uint32_t H = d.hidden, P = d.ple_width, LP = d.layers * d.ple_width;
+    hipStream_t st = s->stream;
+    I32GemvArgs ig{};
+    {
         const LayerWeights& L = m->layers[l];
         const uint32_t hd = L.head_dim, qw = L.q_rows, kvw = L.kv_rows, qkvw = qw + 2 * kvw;
         // 1. q|k|v = W_qkv rms_norm(x, input_layernorm)  (project_tokens :497-579)
@@ -683,6 +709,14 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
         RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
         RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ple, d.norm_eps, s->attended, H, L.layer_scalar,
                                            s->x, H, H, rows, st));
+    }
+    return 0;
+}
+
+static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+    RT_CHECK(gemma_ple(s, rows));
+    for (uint32_t l = 0; l < s->model->d.layers; l++) {
+        RT_CHECK(gemma_layer(s, l, rows));
         RT_CHECK(checkpoint_layer(s, sink, l, rows));
     }
     return 0;
@@ -737,16 +771,61 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     return 0;
 }
 
-static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t count) {
+// The pass's rows: the embedding of `ids` at positions start.., the step
+// counter reset.
+static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t count, uint32_t start = 0) {
     IrisModel* m = s->model;
     s->rope_ready = false;
     for (uint32_t i = 0; i < count; i++)
         if (ids[i] < 0 || (uint32_t)ids[i] >= m->d.vocab) return IRIS_E_INVALID;
-    RT_CHECK(hipMemsetAsync(s->d_pos, 0, sizeof(int32_t), s->stream));
-    RT_CHECK(hipMemsetAsync(s->d_step, 0, sizeof(int32_t), s->stream));
+    RT_CHECK(iris_set_counters_launch(s->d_pos, (int32_t)start, s->d_step, 0, s->stream));
     RT_CHECK(hipMemcpyAsync(s->ids, ids, (size_t)count * 4, hipMemcpyHostToDevice, s->stream));
     return iris_embed_rows_launch(s->ids, count, m->embed_raw, m->embed_row_bytes, m->d.hidden, m->embed_scale, s->x,
                                   s->stream);
+}
+
+// ---- KV coverage (raster-stages/layer-mistral/src/lib.rs:889-940,
+// raster-stages/prefill-range/src/lib.rs:1237-1290): a range at `start`
+// needs, in its attention source's cache, every position before it that its
+// first row sees: all of 0..start, or for a sliding layer the window's part.
+
+// First position the rows of a range at `start` read from before it.
+static uint32_t range_needs_from(const LayerWeights& L, uint32_t start) {
+    if (L.window == 0 || start == 0) return 0;
+    return start + 1 > L.window ? start + 1 - L.window : 0;
+}
+
+static bool range_covered(const IrisSession* s, uint32_t start) {
+    const IrisModel* m = s->model;
+    for (uint32_t l = 0; l < m->d.layers; l++) {
+        const LayerWeights& L = m->layers[l];
+        const uint32_t src = (uint32_t)L.kv_source;
+        const uint32_t from = range_needs_from(L, start);
+        if (from < start && (s->kv_lo[src] > from || s->kv_hi[src] < start)) return false;
+    }
+    return true;
+}
+
+// Positions [pos0, pos0 + count) of a layer's cache now hold keys; a block
+// that does not touch what the cache held starts it afresh.
+static void cover(IrisSession* s, uint32_t l, uint32_t pos0, uint32_t count) {
+    uint32_t& lo = s->kv_lo[l];
+    uint32_t& hi = s->kv_hi[l];
+    const uint32_t end = pos0 + count;
+    if (lo == hi || pos0 > hi || end < lo) {
+        lo = pos0;
+        hi = end;
+    } else {
+        lo = std::min(lo, pos0);
+        hi = std::max(hi, end);
+    }
+}
+
+static void cover_all(IrisSession* s, uint32_t pos0, uint32_t count, bool fresh) {
+    for (uint32_t l = 0; l < s->model->d.layers; l++) {
+        if (fresh) s->kv_lo[l] = s->kv_hi[l] = 0;
+        cover(s, l, pos0, count);
+    }
 }
 
 // Captures the decode pass (one row, head, select) as a graph. Each
@@ -797,6 +876,8 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     hipError_t st = hipStreamCreate(&s->stream);
     s->k_cache.assign(d.layers, nullptr);
     s->v_cache.assign(d.layers, nullptr);
+    s->kv_lo.assign(d.layers, 0);
+    s->kv_hi.assign(d.layers, 0);
     for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++) {
         const size_t kvw = m->layers[l].kv_rows;
         st = hipMalloc((void**)&s->k_cache[l], (size_t)s->k_pos_stride * kvw * 4);
@@ -907,6 +988,8 @@ int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt
         }
     }
     RT_CHECK(session_reset_and_embed(s, prompt, prompt_len));
+    // The passes fill positions 0..prompt_len + tokens - 1 of every cache.
+    cover_all(s, 0, (uint32_t)end, true);
     RT_CHECK(session_pass(s, prompt_len, nullptr));
     RT_CHECK(session_head_select(s, prompt_len));
     if (use_graph && tokens > 1) RT_CHECK(ensure_graph(s, true));
@@ -949,14 +1032,17 @@ static int ensure_checkpoint_space(IrisSession* s) {
 // the device as it finishes; a second stream brings them to pinned host
 // memory behind it, and host threads hash (and copy out) each layer as it
 // arrives, so the transfers and the hashing overlap the later layers.
-int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, int32_t* out_rows,
-                            uint8_t* out_hashes) {
+int iris_session_layer_range(IrisSession* s, const int32_t* ids, uint32_t count, uint32_t start_position,
+                             int32_t* out_rows, uint8_t* out_hashes) {
     if (!s || !ids || count == 0) return IRIS_E_INVALID;
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
-    if (count > s->max_rows || count > d.max_positions) return IRIS_E_RANGE;
+    const uint64_t end = (uint64_t)start_position + count;
+    if (count > s->max_rows || end > d.max_positions || end > s->max_positions) return IRIS_E_RANGE;
+    if (!range_covered(s, start_position)) return IRIS_E_STATE;
+    cover_all(s, start_position, count, start_position == 0);
     if (!out_rows && !out_hashes) {
-        RT_CHECK(session_reset_and_embed(s, ids, count));
+        RT_CHECK(session_reset_and_embed(s, ids, count, start_position));
         RT_CHECK(session_pass(s, count, nullptr));
         return (int)hipStreamSynchronize(s->stream);
     }
@@ -966,7 +1052,7 @@ int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, 
     hipEvent_t* on_device = s->ckpt_events.data();
     hipEvent_t* on_host = on_device + layers;
     const CkptSink sink{s->ckpt_dev, on_device};
-    RT_CHECK(session_reset_and_embed(s, ids, count));
+    RT_CHECK(session_reset_and_embed(s, ids, count, start_position));
     RT_CHECK(session_pass(s, count, &sink));
     for (uint32_t l = 0; l < layers; l++) {
         RT_CHECK(hipStreamWaitEvent(s->copy_stream, on_device[l], 0));
@@ -994,6 +1080,74 @@ int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, 
     for (auto& th : pool) th.join();
     RT_CHECK(hipStreamSynchronize(s->stream));
     return status;
+}
+
+int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, int32_t* out_rows,
+                            uint8_t* out_hashes) {
+    return iris_session_layer_range(s, ids, count, 0, out_rows, out_hashes);
+}
+
+// One layer over one range (run_layer_stage, mistral/stage.rs:172-226;
+// run_prefill_range_direct, prefill_range.rs:82-172): the layer's input rows
+// come from the host, its output rows go back, and its own keys and values
+// of positions start.. land in the layer's cache beside the carried ones.
+int iris_session_layer_stage(IrisSession* s, uint32_t layer, const int32_t* in_rows, uint32_t count,
+                             uint32_t start_position, const int32_t* ple_rows, int32_t* out_rows) {
+    if (!s || !in_rows || !out_rows || count == 0) return IRIS_E_INVALID;
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
+    if (layer >= d.layers || (gemma && !ple_rows)) return IRIS_E_INVALID;
+    const uint64_t end = (uint64_t)start_position + count;
+    if (count > s->max_rows || end > d.max_positions || end > s->max_positions) return IRIS_E_RANGE;
+    const LayerWeights& L = m->layers[layer];
+    const uint32_t src = (uint32_t)L.kv_source, from = range_needs_from(L, start_position);
+    if (from < start_position && (s->kv_lo[src] > from || s->kv_hi[src] < start_position)) return IRIS_E_STATE;
+    cover(s, layer, start_position, count);
+    s->rope_ready = false;
+    s->ssq_x_valid = false;
+    hipStream_t st = s->stream;
+    const size_t H = d.hidden;
+    RT_CHECK(iris_set_counters_launch(s->d_pos, (int32_t)start_position, s->d_step, 0, st));
+    RT_CHECK(hipMemcpyAsync(s->x, in_rows, (size_t)count * H * 4, hipMemcpyHostToDevice, st));
+    if (gemma) {
+        // The layer's PLE inputs in their column of the pass's PLE rows.
+        const size_t P = d.ple_width, LP = (size_t)d.layers * d.ple_width;
+        RT_CHECK(hipMemcpy2DAsync(s->ple_rows + (size_t)layer * P, LP * 4, ple_rows, P * 4, P * 4, count,
+                                  hipMemcpyHostToDevice, st));
+        RT_CHECK(gemma_layer(s, layer, count));
+    } else {
+        RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, count, s->rope_sc, st));
+        RT_CHECK(mistral_layer(s, layer, count, false, false));
+    }
+    RT_CHECK(hipMemcpyAsync(out_rows, s->x, (size_t)count * H * 4, hipMemcpyDeviceToHost, st));
+    return (int)hipStreamSynchronize(st);
+}
+
+// Carried keys into a layer's cache: one kv row of k and of v per position,
+// the K side transposed into the cache's [kv_rows][k_pos_stride] layout.
+int iris_session_write_kv(IrisSession* s, uint32_t layer, uint32_t pos0, uint32_t count, const int32_t* k,
+                          const int32_t* v) {
+    if (!s || (count && (!k || !v))) return IRIS_E_INVALID;
+    const IrisModelDesc& d = s->model->d;
+    if (layer >= d.layers) return IRIS_E_INVALID;
+    if ((uint64_t)pos0 + count > s->max_positions) return IRIS_E_RANGE;
+    if (count == 0) return 0;
+    const size_t kvw = s->model->layers[layer].kv_rows;
+    std::vector<int32_t> kt;
+    try {
+        kt.resize(kvw * count);
+    } catch (...) {
+        return IRIS_E_NOMEM;
+    }
+    for (size_t p = 0; p < count; p++)
+        for (size_t c = 0; c < kvw; c++) kt[c * count + p] = k[p * kvw + c];
+    RT_CHECK(hipStreamSynchronize(s->stream));
+    RT_CHECK(hipMemcpy2D(s->k_cache[layer] + pos0, (size_t)s->k_pos_stride * 4, kt.data(), (size_t)count * 4,
+                         (size_t)count * 4, kvw, hipMemcpyHostToDevice));
+    RT_CHECK(hipMemcpy(s->v_cache[layer] + (size_t)pos0 * kvw, v, (size_t)count * kvw * 4, hipMemcpyHostToDevice));
+    cover(s, layer, pos0, count);
+    return 0;
 }
 
 // The K cache is transposed ([kv_rows][k_pos_stride]): the block of the
@@ -1029,6 +1183,7 @@ int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, d
     hipEvent_t e0 = nullptr, e1 = nullptr;
     RT_CHECK(hipEventCreate(&e0));
     RT_CHECK(hipEventCreate(&e1));
+    cover_all(s, 0, count, true);
     int rc = session_reset_and_embed(s, ids, count);
     if (rc == 0) rc = (int)hipEventRecord(e0, s->stream);
     if (rc == 0) rc = session_pass(s, count, nullptr);
@@ -1054,6 +1209,7 @@ int iris_session_time_decode(IrisSession* s, const int32_t* prompt, uint32_t pro
     RT_CHECK(hipEventCreate(&e0));
     RT_CHECK(hipEventCreate(&e1));
     RT_CHECK(hipEventCreate(&e2));
+    cover_all(s, 0, (uint32_t)end, true);
     int rc = session_reset_and_embed(s, prompt, prompt_len);
     if (rc == 0) rc = (int)hipEventRecord(e0, s->stream);
     if (rc == 0) rc = session_pass(s, prompt_len, nullptr);

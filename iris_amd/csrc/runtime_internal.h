@@ -67,6 +67,11 @@ struct IrisSession {
     uint32_t k_pos_stride = 0;  // positions per row of the transposed K cache: max_positions rounded up to 64
     hipStream_t stream = nullptr;
     std::vector<int32_t*> k_cache, v_cache;  // per layer [position][kv_heads*head_dim]
+    // Per layer, the positions [kv_lo, kv_hi) its cache holds, as passes and
+    // carried keys (iris_session_write_kv) left them; a range over positions
+    // start.. needs its attention source's cache to hold what the range's
+    // first row sees before `start`.
+    std::vector<uint32_t> kv_lo, kv_hi;
     int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;
     int32_t* scores = nullptr;  // one-row attention: [heads][k_pos_stride]
     // One-row passes: per-tile sums of squares of x and attended, written by

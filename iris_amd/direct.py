@@ -50,6 +50,9 @@ def _declare():
         "iris_session_free": (None, [vp]),
         "iris_session_generate": (C.c_int, [vp, vp, u32, u32, vp, u32, vp, C.POINTER(u32), vp, i32]),
         "iris_session_layer_pass": (C.c_int, [vp, vp, u32, vp, vp]),
+        "iris_session_layer_range": (C.c_int, [vp, vp, u32, u32, vp, vp]),
+        "iris_session_layer_stage": (C.c_int, [vp, u32, vp, u32, u32, vp, vp]),
+        "iris_session_write_kv": (C.c_int, [vp, u32, u32, u32, vp, vp]),
         "iris_session_time_decode": (C.c_int, [vp, vp, u32, u32, C.POINTER(C.c_double), C.POINTER(C.c_double), vp]),
         "iris_session_time_pass": (C.c_int, [vp, vp, u32, C.POINTER(C.c_double)]),
         "iris_session_read_kv": (C.c_int, [vp, u32, u32, u32, vp, vp]),
@@ -187,6 +190,42 @@ class Session:
                                                           rows.ctypes.data if keep_rows else None,
                                                           hashes.ctypes.data), "layer pass")
         return rows, [bytes(h).hex() for h in hashes]
+
+    def layer_range(self, ids, start_position: int, keep_rows: bool = True):
+        """The chain pass over one range at ``start_position`` over the keys
+        the caches hold for the positions before it: (rows [layers, n,
+        hidden] or None, SHA-256 per layer). Raises IrisError (IRIS_E_STATE)
+        when a cache lacks a position the range needs."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        m = self.dm.model
+        rows = np.zeros((m.num_layers, ids.size, m.hidden), dtype=np.int32) if keep_rows else None
+        hashes = np.zeros((m.num_layers, 32), dtype=np.uint8)
+        native.check(native.lib().iris_session_layer_range(self._h, ids.ctypes.data, ids.size, start_position,
+                                                           rows.ctypes.data if keep_rows else None,
+                                                           hashes.ctypes.data), "layer range")
+        return rows, [bytes(h).hex() for h in hashes]
+
+    def layer_stage(self, layer: int, in_rows, start_position: int, ple_rows=None):
+        """One layer over one range: the layer's output rows [n, hidden] for
+        input rows [n, hidden] at start_position.. (gemma-dense: with the
+        layer's PLE rows [n, ple_width])."""
+        x = np.ascontiguousarray(in_rows, dtype=np.int32)
+        out = np.empty_like(x)
+        ple = None if ple_rows is None else np.ascontiguousarray(ple_rows, dtype=np.int32)
+        native.check(native.lib().iris_session_layer_stage(self._h, layer, x.ctypes.data, x.shape[0], start_position,
+                                                           None if ple is None else ple.ctypes.data,
+                                                           out.ctypes.data), f"layer {layer} stage")
+        return out
+
+    def write_kv(self, layer: int, pos0: int, k, v):
+        """Carried keys into a layer's cache: rows [count, kv_heads*head_dim]
+        of k and v for positions pos0.. (the reference's KeyRow k and v)."""
+        k = np.ascontiguousarray(k, dtype=np.int32)
+        v = np.ascontiguousarray(v, dtype=np.int32)
+        if k.shape != v.shape or k.ndim != 2:
+            raise ValueError("k and v must be [count, kv_width] arrays of one shape")
+        native.check(native.lib().iris_session_write_kv(self._h, layer, pos0, k.shape[0], k.ctypes.data,
+                                                        v.ctypes.data), "write kv")
 
     def time_decode(self, prompt_ids, steps: int):
         """(ms per decode token, prefill ms, generated ids) from HIP events."""
