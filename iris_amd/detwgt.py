@@ -30,7 +30,8 @@ class Tensor:
     name: str
     dims: tuple
     width: int
-    payload: bytes
+    payload: object  # bytes or a view of a mapping
+    offset: int = 0  # of the payload in the artifact
 
     def values(self) -> np.ndarray:
         """Q16.16 values as int32 (widths 16 and 32)."""
@@ -104,18 +105,20 @@ def write(tensors) -> bytes:
     return bytes(out)
 
 
-def read(buf: bytes) -> dict:
+def read(buf) -> dict:
     """Parse a DETWGT v2/v3 artifact into {name: Tensor}, with the reader's
-    checks (crates/model/detwgt/src/mmap.rs:462-529)."""
+    checks (crates/model/detwgt/src/mmap.rs:462-529). ``buf`` is bytes or
+    any buffer (a mapping): payloads are views into it, not copies."""
     mv = memoryview(buf)
+    n = len(mv)
     off = 0
 
-    def take(n):
+    def take(k):
         nonlocal off
-        if off + n > len(buf):
+        if off + k > n:
             raise ValueError("detwgt artifact is truncated")
-        s = mv[off:off + n]
-        off += n
+        s = mv[off:off + k]
+        off += k
         return s
 
     if bytes(take(8)) != MAGIC:
@@ -146,12 +149,52 @@ def read(buf: bytes) -> dict:
         if plen != expected:
             raise ValueError(f"tensor '{name}' payload length does not match its width")
         off += -off % ALIGN
-        if off > len(buf):
+        if off > n:
             raise ValueError("detwgt artifact is truncated")
-        payload = bytes(take(plen))
+        at = off
+        payload = take(plen)
         if name in tensors:
             raise ValueError(f"duplicate tensor '{name}' in artifact")
-        tensors[name] = Tensor(name, tuple(dims), width, payload)
-    if off != len(buf):
+        tensors[name] = Tensor(name, tuple(dims), width, payload, at)
+    if off != n:
         raise ValueError("trailing bytes after the last tensor payload")
     return tensors
+
+
+class MappedDetwgt:
+    """A DETWGT file mapped read-only (MmapDetwgt::open,
+    crates/model/detwgt/src/mmap.rs): the directory is parsed with read()'s
+    checks and every tensor's payload is a view of the mapping, so the
+    weights are paged in from the file as they are used, never copied
+    whole. ``key(name)`` names a tensor's bytes for as long as the mapping
+    lives (the reference's Q8Key::mapped(mapping, offset),
+    crates/inference/kernels/src/tensor.rs:90-108)."""
+
+    _next_mapping = 1
+
+    def __init__(self, path: str):
+        import mmap
+        self.path = path
+        self._file = open(path, "rb")
+        try:
+            self._map = mmap.mmap(self._file.fileno(), 0, access=mmap.ACCESS_READ)
+        except ValueError:  # an empty file cannot be mapped
+            self._file.close()
+            raise ValueError("not a detwgt artifact")
+        self.mapping = MappedDetwgt._next_mapping
+        MappedDetwgt._next_mapping += 1
+        self.tensors = read(memoryview(self._map))
+
+    def key(self, name: str) -> tuple:
+        return (self.mapping, self.tensors[name].offset)
+
+    def close(self):
+        self.tensors = {}
+        if self._map is not None:
+            try:
+                self._map.close()
+            except BufferError:
+                pass  # views still alive keep the mapping until they go
+            self._map = None
+        self._file.close()
+

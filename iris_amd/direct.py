@@ -126,6 +126,23 @@ class DeviceModel:
             self.free()
             raise
 
+    @classmethod
+    def from_manifest(cls, manifest_path: str) -> "DeviceModel":
+        """The model a verified manifest names (ModelManifest::load_verified,
+        crates/inference/artifacts/src/direct.rs:135-177), its DETWGT mapped
+        and uploaded tensor by tensor from the mapping
+        (DirectInferenceModel::load, crates/inference/direct/src/model.rs:
+        167-233). ``.manifest`` keeps the manifest."""
+        from . import artifacts
+        manifest, model, mapped = artifacts.load_model(manifest_path)
+        try:
+            dm = cls(model)
+        finally:
+            model.tensors = {}
+            mapped.close()
+        dm.manifest = manifest
+        return dm
+
     def _set(self, name, width, arr, rows, cols):
         arr = np.ascontiguousarray(arr)
         native.check(native.lib().iris_model_set_tensor(self._h, name.encode(), width, arr.ctypes.data, rows, cols),

@@ -70,6 +70,43 @@ class Q8Matrix:
             pass
 
 
+class UploadCache:
+    """Device copies of Q8_0 matrices by the key that names their bytes (the
+    reference's Q8Key, crates/inference/kernels/src/tensor.rs:90-108: a
+    mapped tensor's (mapping, offset), or a unique key), evicting the least
+    recently used once the held bytes pass ``budget`` (the reference's
+    device cache, crates/inference/kernels/src/gpu.rs:176-208)."""
+
+    def __init__(self, budget: int = 64 << 30):
+        from collections import OrderedDict
+        self.budget = budget
+        self.held = 0
+        self._items = OrderedDict()
+        self.uploads = 0
+
+    def get(self, key, raw: np.ndarray, rows: int, cols: int) -> Q8Matrix:
+        m = self._items.get(key)
+        if m is not None:
+            self._items.move_to_end(key)
+            return m
+        m = Q8Matrix.from_bytes(raw, rows, cols)
+        self.uploads += 1
+        size = m.info()["bytes"]
+        self._items[key] = m
+        self.held += size
+        while self.held > self.budget and len(self._items) > 1:
+            _, old = self._items.popitem(last=False)
+            self.held -= old.info()["bytes"]
+            old.free()
+        return m
+
+    def clear(self):
+        for m in self._items.values():
+            m.free()
+        self._items.clear()
+        self.held = 0
+
+
 def linear_slab_from_source(inp: np.ndarray, matrix: Q8Matrix) -> np.ndarray:
     """out[t][r] = dot_row(inp[t], W[r]) for every token row of ``inp``."""
     inp = np.ascontiguousarray(np.atleast_2d(inp), dtype=np.int32)

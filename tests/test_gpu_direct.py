@@ -4,6 +4,7 @@ without graph replay, for both families: small models, the reference's
 parity bundle cases (EOS included), and the Mistral-7B and Gemma-2B shapes;
 plus the teacher-forced per-layer pass (rows and per-layer SHA-256)."""
 import hashlib
+import os
 
 import numpy as np
 import pytest
@@ -214,3 +215,55 @@ def test_non_finite_embedding_scale_is_refused(family, name):
     with pytest.raises(native.IrisError) as e:
         DeviceModel(m)
     assert e.value.code == -2
+
+
+@pytest.mark.parametrize("family", ["mistral-dense", "gemma-dense"])
+def test_model_from_a_verified_manifest(tmp_path, family):
+    # A bundle written to disk, verified by its manifest, mapped and uploaded
+    # tensor by tensor: generation equals the oracle over the same bytes.
+    from iris_amd import artifacts
+    if family == "mistral-dense":
+        buf, shape, cases = synth.parity_mistral_detwgt(), synth.parity_mistral_shape(), "parity-mistral"
+    else:
+        buf, shape, cases = synth.parity_gemma_detwgt(), synth.parity_gemma_shape(), "parity-gemma"
+    g = golden("parity_bundles.json")["bundles"][cases]
+    sd = dict(vars(shape))
+    if family == "gemma-dense":
+        sd.pop("tied_head")
+    path = artifacts.write_bundle(str(tmp_path), buf, family, sd, eos_token_ids=g["eos_token_ids"],
+                                  config={"text_config": {"tie_word_embeddings": bool(shape.tied_head)}})
+    dm = DeviceModel.from_manifest(path)
+    assert dm.manifest.family == family
+    c = g["cases"][2]
+    s = Session(dm, 128, 64)
+    got = s.generate(c["input_token_ids"], c["tokens"], keep_logits=True)
+    m = model_mod.from_detwgt(buf, family, shape, eos_token_ids=g["eos_token_ids"])
+    want_tokens, want_logits = _oracle_generate(m, c["input_token_ids"], c["tokens"], 128)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
+    s.free()
+    dm.free()
+
+
+def test_upload_cache_by_mapped_key(tmp_path):
+    # Products over a mapped DETWGT through the drop-in ABI, uploads cached
+    # by (mapping, offset): each matrix goes to the device once, and every
+    # product equals the oracle's dot_row slab.
+    from iris_amd import detwgt, tensor
+    path = os.path.join(str(tmp_path), "model.detwgt")
+    with open(path, "wb") as f:
+        f.write(synth.parity_mistral_detwgt())
+    mapped = detwgt.MappedDetwgt(path)
+    cache = tensor.UploadCache()
+    names = [n for n, t in mapped.tensors.items() if t.width == detwgt.Q8_0_WIDTH][:6]
+    rng = np.random.default_rng(3)
+    for rep in range(2):
+        for n in names:
+            raw = mapped.tensors[n].q8()
+            rows, cols = raw.shape[0], raw.shape[1] // 34 * 32
+            mat = cache.get(mapped.key(n), raw, rows, cols)
+            x = rng.integers(-(1 << 20), 1 << 20, (3, cols)).astype(np.int32)
+            assert np.array_equal(tensor.linear_slab_from_source(x, mat), cpu.linear_q8(x, raw)), n
+    assert cache.uploads == len(names)
+    cache.clear()
+    mapped.close()
