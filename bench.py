@@ -123,6 +123,12 @@ def main():
 
     roof = gemv_roofline(decode_timing)
     log(f"GEMV {roof['avg_launch_us']} us = {roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of peak)")
+    gpb = decode_timing.time_gemv(per_row_scale=False)
+    gemv_pb = {"launch": "Q8_0 GEMV M=1 K=4096 N=14336, one f16 scale per block",
+               "avg_launch_us": round(gpb["us"], 3), "algorithmic_bytes": gpb["algorithmic_bytes"],
+               "achieved": round(gpb["algorithmic_bytes"] / (gpb["us"] * 1e-6) / 1e9, 1), "unit": "GB/s"}
+    gemv_pb["frac"] = round(gemv_pb["achieved"] / PEAK_HBM_GBPS, 4)
+    log(f"GEMV per-block scales {gemv_pb['avg_launch_us']} us = {gemv_pb['achieved']} GB/s")
 
     # The teacher-forced chain pass (2048 rows, per-layer checkpoint hashes)
     # on the same model, and its largest product on the int8 matrix cores.
@@ -132,6 +138,9 @@ def main():
     bench.dm.free()
     gemm = decode_timing.time_gemm(TEACHER_FORCED_ROWS)
     log(f"MFMA GEMM {gemm['shape']}: {gemm['us']} us = {gemm['mfma_tops']} TOP/s ({100 * gemm['frac']:.1f}% of int8 peak)")
+    gemm_pb = decode_timing.time_gemm(TEACHER_FORCED_ROWS, per_row_scale=False)
+    log(f"MFMA GEMM per-block scales {gemm_pb['shape']}: {gemm_pb['us']} us, {gemm_pb['weight_planes']} weight planes "
+        f"= {gemm_pb['mfma_tops']} TOP/s ({100 * gemm_pb['frac']:.1f}% of int8 peak)")
 
     base = None
     if not args.no_cpu:
@@ -147,13 +156,15 @@ def main():
         "config": {"workload": "mistral-7b-shape Q8_0 greedy decode, prompt 512 + 512 tokens, batch 1",
                    "prompt_tokens": PROMPT, "decode_steps_timed": args.steps, "batch": 1},
         "roofline": roof,
+        "gemv_per_block": gemv_pb,
         "decode_roofline": {"bound": "hbm", "achieved": round(decode_gbps, 1), "peak": PEAK_HBM_GBPS,
                             "unit": "GB/s", "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
                             "bytes_per_token": int(per_token)},
         "prompt_pass_ms": round(prefill_ms, 2),
         "deterministic_rerun": deterministic,
         "teacher_forced": dict(tf, workload="mistral-7b-shape chain pass over 2048 uniform ids, "
-                                            "per-layer SHA-256 checkpoints", mfma_gemm=gemm),
+                                            "per-layer SHA-256 checkpoints", mfma_gemm=gemm,
+                                 mfma_gemm_per_block=gemm_pb),
         "cpu_baseline": base,
     }
     print(json.dumps(line), flush=True)

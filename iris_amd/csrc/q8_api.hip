@@ -194,6 +194,8 @@ void q8gpu_free(Q8GpuMatrix* m) {
     hipFree(m->sc16);
     hipFree(m->sc64);
     hipFree(m->row_scale);
+    hipFree(m->fold.planes);
+    hipFree(m->fold.shift);
     std::free(m);
 }
 
@@ -277,8 +279,13 @@ uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* m, uint32_t tokens) {
     return planes_bytes(m->cols, tokens) + 8ull * tokens;
 }
 
-int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
-                            void* d_workspace, uint64_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+// The product with optional work space; `may_fold` lets a per-block scale
+// matrix be folded for the matrix cores (which allocates) on its first
+// multi-token product.
+static int product_with_space(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
+                              void* d_workspace, uint64_t workspace_bytes, void* stream, bool may_fold) {
     if (!m || (tokens && (!d_act || !d_out))) return IRIS_E_INVALID;
     GemvArgs a{};
     a.w = q8_view(m);
@@ -291,10 +298,22 @@ int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t
     a.out_stride = m->rows;
     if (d_workspace && tokens >= 2) {
         if (workspace_bytes < q8gpu_workspace_bytes(m, tokens)) return IRIS_E_RANGE;
+        if (may_fold) {
+            const int rc = iris_q8_prepare_fold(const_cast<Q8GpuMatrix*>(m), (hipStream_t)stream);
+            if (rc != 0) return rc;
+            a.w = q8_view(m);
+        }
         a.planes = (int8_t*)d_workspace;
         a.token_limbs = (int32_t*)((char*)d_workspace + planes_bytes(m->cols, tokens));
     }
     return iris_gemv_launch(a, (hipStream_t)stream);
+}
+
+extern "C" {
+
+int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
+                            void* d_workspace, uint64_t workspace_bytes, void* stream) {
+    return product_with_space(m, d_act, tokens, d_out, d_workspace, workspace_bytes, stream, true);
 }
 
 // q8gpu_product_device_ws with the device's scratch array as the work space:
@@ -310,7 +329,7 @@ int q8gpu_product_device_noalloc(const Q8GpuMatrix* m, const int32_t* d_act, uin
     uint8_t* ws = nullptr;
     const int rc = scratch_for_current_device(&ws);
     if (rc != 0) return rc;
-    return q8gpu_product_device_ws(m, d_act, tokens, d_out, ws, IRIS_NOALLOC_SCRATCH_BYTES, stream);
+    return product_with_space(m, d_act, tokens, d_out, ws, IRIS_NOALLOC_SCRATCH_BYTES, stream, false);
 }
 
 int q8gpu_product(const Q8GpuMatrix* m, const int32_t* activations, uint32_t tokens, int32_t* out) {

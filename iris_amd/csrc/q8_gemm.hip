@@ -24,6 +24,8 @@
 // own 16 bytes, the wave writes one contiguous kilobyte, no registers in
 // between) through a four-deep ring of 64-wide k steps, and read back by
 // each lane as one conflict-free 16-byte LDS load.
+#include <mutex>
+
 #include "detnum_dev.h"
 #include "q8_epilogue.h"
 #include "q8_internal.h"
@@ -45,6 +47,7 @@ constexpr uint32_t GM_BAND = 8;             // row groups per band of the launch
 template <uint32_t W>
 struct GemmShape {
     static constexpr uint32_t WAVES = W, THREADS = 64 * W, RT = W;  // RT: 32-row tiles
+    static constexpr int RI = 2;                                      // row tiles per wave
     static constexpr uint32_t STAGE = (2 * W + 24) * FRAG;
     static constexpr uint32_t STAGES = W == 8 ? 3 : 4;
     static constexpr uint32_t OUT = 32 * W * 129 * 4;  // the output block, [row][128 tokens + 1]
@@ -232,12 +235,14 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
 }
 
 // Output e of lane l of a 32 x 32 block is row 8(e/4) + 4(l/32) + e%4,
-// token l % 32: recombine the planes, scale, round once (and, for the
-// gated activations, combine each gate/up row pair in registers), park the
-// block in LDS as [row][token], then run the epilogue row-fastest.
-template <class G, int LG, int TTW>
-__device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
-                                              const v16i (&acc)[2][TTW][LG]) {
+// token l % 32. Each wave's blocks (row tiles wr*2 + i, token tiles wt*TTW
+// + j) get their values from `block_values(i, j, v)`, rounded once (and,
+// for the gated activations, each gate/up row pair combined in registers);
+// the blocks are parked in LDS as [row][token], then the epilogue runs
+// row-fastest.
+template <class G, int TTW, class Values>
+__device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
+                                               Values&& block_values) {
     constexpr uint32_t NTOK = 64 * TTW, ROWS = G::RT * 32, STRIDE = NTOK + 1;
     static_assert(ROWS * STRIDE * 4 <= G::SMEM, "output block must fit the LDS");
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -246,52 +251,25 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
     const bool pairs = a.epilogue == EPI_SWIGLU || a.epilogue == EPI_GEGLU;
     int32_t* sC = (int32_t*)smem;
 #pragma unroll
-    for (int i = 0; i < 2; i++) {
+    for (int i = 0; i < G::RI; i++) {
 #pragma unroll
         for (int j = 0; j < TTW; j++) {
             const uint32_t tl = (wt * TTW + j) * 32 + (lane & 31);
             int32_t v[16];
-            // round_to_i32(tot * scale, 24) (q8.rs:94-104) through one 64-bit
-            // product where the operands' bit lengths show it cannot
-            // overflow (the usual case); if any lane of the wave has a
-            // larger product, the wave redoes the block with 128-bit ones.
-            bool fits = true;
-#pragma unroll
-            for (int e = 0; e < 16; e++) {
-                const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4), row = rt0 * 32 + rl;
-                int64_t tot = 0;  // the row's integer dot product, |tot| < K * 2^38
-#pragma unroll
-                for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
-                const int64_t sc = row < w.rows ? w.row_scale[row] : 0;
-                const uint64_t at = tot < 0 ? 0 - (uint64_t)tot : (uint64_t)tot;
-                const uint64_t as = sc < 0 ? 0 - (uint64_t)sc : (uint64_t)sc;
-                fits &= (128 - __clzll(at) - __clzll(as)) <= 63;  // |tot * sc| < 2^63
-                v[e] = dn::clamp_i64_to_i32(dn::rshift_rte((int64_t)((uint64_t)tot * (uint64_t)sc), 24));
-            }
-            if (!__all(fits)) {
-#pragma unroll
-                for (int e = 0; e < 16; e++) {
-                    const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4),
-                                   row = rt0 * 32 + rl;
-                    int64_t tot = 0;
-#pragma unroll
-                    for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
-                    v[e] = row < w.rows ? dn::round_to_i32((dn::i128)tot * (dn::i128)w.row_scale[row], 24) : 0;
-                }
-            }
+            block_values(i, j, v);
             if (pairs) {
                 // Rows e and e + 1 (e even) are a gate/up pair in this lane:
                 // the activation runs here, once per pair, every lane busy.
 #pragma unroll
                 for (int e = 0; e < 16; e += 2) {
-                    const uint32_t rl = (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                    const uint32_t rl = (wr * G::RI + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
                     const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v[e]) : dn::gelu(v[e]);
                     sC[(rl >> 1) * STRIDE + tl] = dn::mul_sat(act, v[e + 1]);
                 }
             } else {
 #pragma unroll
                 for (int e = 0; e < 16; e++)
-                    sC[((wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4)) * STRIDE + tl] = v[e];
+                    sC[((wr * G::RI + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4)) * STRIDE + tl] = v[e];
             }
         }
     }
@@ -329,6 +307,43 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
         }
     }
     __syncthreads();
+}
+
+// Row-scale matrices: the planes recombine into the row's integer dot
+// product, then round_to_i32(tot * scale, 24) (q8.rs:94-104) through one
+// 64-bit product where the operands' bit lengths show it cannot overflow
+// (the usual case); if any lane of the wave has a larger product, the wave
+// redoes the block with 128-bit ones.
+template <class G, int LG, int TTW>
+__device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
+                                              const v16i (&acc)[2][TTW][LG]) {
+    const uint32_t lane = threadIdx.x & 63, wr = (threadIdx.x >> 6) % (G::WAVES / 2);
+    const Q8View& w = a.w;
+    park_and_store<G, TTW>(a, smem, rt0, tt0, [&](int i, int j, int32_t (&v)[16]) __attribute__((always_inline)) {
+        bool fits = true;
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t row = rt0 * 32 + (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+            int64_t tot = 0;  // the row's integer dot product, |tot| < K * 2^38
+#pragma unroll
+            for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
+            const int64_t sc = row < w.rows ? w.row_scale[row] : 0;
+            const uint64_t at = tot < 0 ? 0 - (uint64_t)tot : (uint64_t)tot;
+            const uint64_t as = sc < 0 ? 0 - (uint64_t)sc : (uint64_t)sc;
+            fits &= (128 - __clzll(at) - __clzll(as)) <= 63;  // |tot * sc| < 2^63
+            v[e] = dn::clamp_i64_to_i32(dn::rshift_rte((int64_t)((uint64_t)tot * (uint64_t)sc), 24));
+        }
+        if (!__all(fits)) {
+#pragma unroll
+            for (int e = 0; e < 16; e++) {
+                const uint32_t row = rt0 * 32 + (wr * 2 + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+                int64_t tot = 0;
+#pragma unroll
+                for (int l = 0; l < LG; l++) tot += (int64_t)acc[i][j][l][e] * ((int64_t)1 << (8 * l));
+                v[e] = row < w.rows ? dn::round_to_i32((dn::i128)tot * (dn::i128)w.row_scale[row], 24) : 0;
+            }
+        }
+    });
 }
 
 template <class G, int LG, int TTW>
@@ -387,11 +402,255 @@ __global__ __launch_bounds__(64 * W, 1) void q8_gemm_row_kernel(const GemvArgs a
     }
 }
 
+
+// ---- per-block scales on the matrix cores ----
+//
+// A per-block scale matrix is first folded (iris_q8_prepare_fold): with
+// s_b = sign_b * m_b * 2^sh_b the exact Q.24 value of block b's f16 scale
+// (m_b the integer significand, under 2^11) and R the least sh_b of the
+// row's non-zero scales, w' = q * sign_b * (m_b << (sh_b - R)) are integers,
+// and dot_row's total sum_b s_b * sum_j q_j x_j equals 2^R * sum_k w'_k x_k
+// (crates/det-num/src/q8.rs:56-72). Each w' is split into WP signed byte
+// digits like the activations, so every (weight digit p, activation digit
+// l) pair is an int8 GEMM with exact int32 sums, and pairs with the same
+// p + l share an accumulator (at most four terms of |.| <= K * 2^14 each,
+// below 2^31 for K <= 16384). The epilogue recombines the shifts in 128
+// bits, shifts by R and rounds once at 24 fraction bits.
+
+// Per row: R (the least exponent shift of its non-zero block scales; 0 for
+// an all-zero row) into shift[row], and the digits its largest |w'| needs
+// raised into *need (more than Q8_FOLD_MAX_PLANES: the row cannot fold).
+__global__ __launch_bounds__(256) void fold_rows_kernel(const uint8_t* qs, const uint16_t* sc16, uint32_t rows,
+                                                        uint32_t nb, int32_t* shift, int* need) {
+    const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    const uint32_t tile = row / Q8_TILE_ROWS, r = row % Q8_TILE_ROWS;
+    const uint16_t* sc = sc16 + (size_t)tile * nb * Q8_TILE_ROWS + r;
+    int least = 64;
+    for (uint32_t b = 0; b < nb; b++) {
+        const uint32_t bits = sc[(size_t)b * Q8_TILE_ROWS], e = (bits >> 10) & 0x1f, mant = bits & 0x3ff;
+        if (e == 0 && mant == 0) continue;
+        least = min(least, e ? (int)e - 1 : 0);
+    }
+    if (least == 64) least = 0;
+    shift[row] = least;
+    int digits = 1;
+    const uint8_t* q = qs + (size_t)tile * nb * Q8_TILE_BLOCK_BYTES + r * 16;
+    for (uint32_t b = 0; b < nb; b++) {
+        const uint32_t bits = sc[(size_t)b * Q8_TILE_ROWS], e = (bits >> 10) & 0x1f, mant = bits & 0x3ff;
+        const int64_t m = (int64_t)(e ? 1024 + mant : mant);
+        if (m == 0) continue;
+        const int d = (e ? (int)e - 1 : 0) - least;
+        if (d > 20) {
+            digits = 5;
+            break;
+        }
+        // The largest |q| of the block (both signs: digits are asymmetric).
+        int qmax = 0, qmin = 0;
+        const uint8_t* qb = q + (size_t)b * Q8_TILE_BLOCK_BYTES;
+        for (int h = 0; h < 2; h++)
+            for (int j = 0; j < 16; j++) {
+                const int v = (int8_t)qb[h * 256 + j];
+                qmax = max(qmax, v);
+                qmin = min(qmin, v);
+            }
+        const int64_t f = (bits & 0x8000) ? -(m << d) : (m << d);
+        for (int64_t wv : {f * qmax, f * qmin}) {
+            const uint64_t dg = (uint64_t)(wv + 0x8080808080LL) ^ 0x8080808080ULL;
+            const int n = (dg >> 32) ? 5 : (dg >> 24) ? 4 : (dg >> 16) ? 3 : (dg >> 8) ? 2 : 1;
+            digits = max(digits, n);
+        }
+    }
+    atomicMax(need, digits);
+}
+
+// One thread per (row, block): the block's w' as `nplanes` digit planes in
+// the qs tile layout.
+__global__ __launch_bounds__(256) void fold_planes_kernel(const uint8_t* qs, const uint16_t* sc16, uint32_t rows,
+                                                          uint32_t nb, const int32_t* shift, uint32_t nplanes,
+                                                          size_t plane_bytes, int8_t* planes) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)rows * nb) return;
+    const uint32_t row = (uint32_t)(idx / nb), b = (uint32_t)(idx % nb);
+    const uint32_t tile = row / Q8_TILE_ROWS, r = row % Q8_TILE_ROWS;
+    const uint32_t bits = sc16[((size_t)tile * nb + b) * Q8_TILE_ROWS + r], e = (bits >> 10) & 0x1f,
+                   mant = bits & 0x3ff;
+    const int64_t m = (int64_t)(e ? 1024 + mant : mant);
+    const int d = m ? (e ? (int)e - 1 : 0) - shift[row] : 0;
+    const int64_t f = (bits & 0x8000) ? -(m << d) : (m << d);
+    const size_t off = ((size_t)tile * nb + b) * Q8_TILE_BLOCK_BYTES + r * 16;
+    for (int h = 0; h < 2; h++) {
+        const uint4 qv = *(const uint4*)(qs + off + h * 256);
+        const uint32_t qw[4] = {qv.x, qv.y, qv.z, qv.w};
+        uint32_t out[Q8_FOLD_MAX_PLANES][4];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            uint64_t dg[4];
+#pragma unroll
+            for (int k = 0; k < 4; k++)
+                dg[k] = (uint64_t)((int64_t)(int8_t)(qw[c] >> (8 * k)) * f + 0x8080808080LL) ^ 0x8080808080ULL;
+#pragma unroll
+            for (uint32_t p = 0; p < Q8_FOLD_MAX_PLANES; p++) out[p][c] = plane_byte4(dg[0], dg[1], dg[2], dg[3], p);
+        }
+        for (uint32_t p = 0; p < nplanes; p++)
+            *(uint4*)(planes + p * plane_bytes + off + h * 256) = make_uint4(out[p][0], out[p][1], out[p][2], out[p][3]);
+    }
+}
+
+// Workgroup shape of the folded product: four waves in a 2 x 2 grid over
+// 128 weight rows and 64 tokens (one wave per SIMD: the shared-shift
+// accumulators, 2 x (WP + LG - 1) blocks per wave, may need the
+// accumulation registers); a stage is one 64-wide k step of WP weight
+// planes and LG activation planes.
+template <int WP, int LG>
+struct FoldShape {
+    // Two row tiles per wave up to three weight planes; one for four (whose
+    // accumulators would not fit twice).
+    static constexpr int RI = WP <= 3 ? 2 : 1;
+    static constexpr uint32_t WAVES = 4, THREADS = 256, RT = 2 * RI;
+    static constexpr uint32_t CHUNKS = 2 * RT * WP + 2 * LG * 2;
+    static constexpr uint32_t PER_WAVE = (CHUNKS + WAVES - 1) / WAVES;
+    static constexpr uint32_t STAGE = PER_WAVE * WAVES * FRAG;
+    static constexpr uint32_t STAGES = 3 * STAGE <= 160 * 1024 ? 3 : 2;
+    static constexpr uint32_t OUT = 32 * RT * 65 * 4;
+    static constexpr uint32_t SMEM = STAGES * STAGE > OUT ? STAGES * STAGE : OUT;
+    static constexpr int NS = WP + LG - 1;
+};
+
+template <class G, int WP, int LG>
+__device__ __forceinline__ void fold_mainloop(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
+                                              v16i (&acc)[G::RI][G::NS]) {
+    constexpr uint32_t TTWG = 2, RT = G::RT, CHUNKS = G::CHUNKS, PER_WAVE = G::PER_WAVE;
+    constexpr uint32_t STAGES = G::STAGES, STAGE = G::STAGE;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t wr = wave % 2, wt = wave / 2;
+    const Q8View& w = a.w;
+    const uint32_t KS = w.cols / 64, KB = w.cols / 32, TT = (a.tokens + 31) / 32;
+    const size_t lstride = (size_t)TT * KB * FRAG;
+    const size_t pstride = (size_t)w.tiles * w.nb * Q8_TILE_BLOCK_BYTES;
+    // Wave w copies chunks w, w + 4, ...: weight-plane operands (1 KB of the
+    // tile layout per k step) first, then digit-plane operands (2 KB).
+    const int8_t* src[PER_WAVE];
+    uint32_t step[PER_WAVE];
+#pragma unroll
+    for (uint32_t i = 0; i < PER_WAVE; i++) {
+        const uint32_t c0 = wave + G::WAVES * i, c = c0 < CHUNKS ? c0 : 0;
+        if (c < 2 * RT * WP) {
+            const uint32_t p = c / (2 * RT), cw = c % (2 * RT), rr = lane & 31, h = lane >> 5, sub = cw & 1;
+            const uint32_t tile16 = min(2 * (rt0 + cw / 2) + rr / 16, w.tiles - 1);
+            src[i] = w.fold_planes + p * pstride + ((size_t)tile16 * w.nb + sub) * Q8_TILE_BLOCK_BYTES + h * 256 +
+                     (rr % 16) * 16;
+            step[i] = FRAG;
+        } else {
+            const uint32_t b = c - 2 * RT * WP, sub = b & 1, rest = b >> 1, l = rest / TTWG;
+            const uint32_t tile = min(tt0 + rest % TTWG, TT - 1);
+            src[i] = a.planes + l * lstride + ((size_t)tile * KB + sub) * FRAG + lane * 16;
+            step[i] = 2 * FRAG;
+        }
+    }
+    auto issue = [&](uint32_t ks) {
+        int8_t* base = smem + (ks % STAGES) * STAGE;
+#pragma unroll
+        for (uint32_t i = 0; i < PER_WAVE; i++)
+            __builtin_amdgcn_global_load_lds(src[i] + (size_t)ks * step[i],
+                                             (__attribute__((address_space(3))) void*)(base + (wave + G::WAVES * i) * FRAG),
+                                             16, 0, 0);
+    };
+#pragma unroll
+    for (uint32_t s = 0; s < STAGES - 1; s++)
+        if (s < KS) issue(s);
+    for (uint32_t ks = 0; ks < KS; ks++) {
+        if (STAGES >= 3 && ks + 2 < KS) wait_vmem<(STAGES >= 3 ? 1 : 0) * PER_WAVE>();
+        else wait_vmem<0>();
+        lds_barrier();
+        if (ks + STAGES - 1 < KS) issue(ks + STAGES - 1);
+        const int8_t* st = smem + (ks % STAGES) * STAGE + lane * 16;
+#pragma unroll
+        for (uint32_t sub = 0; sub < 2; sub++) {
+            v4i fa[G::RI][WP];
+#pragma unroll
+            for (int i = 0; i < G::RI; i++)
+#pragma unroll
+                for (int p = 0; p < WP; p++)
+                    fa[i][p] = *(const v4i*)(st + (p * 2 * RT + 2 * (wr * G::RI + i) + sub) * FRAG);
+#pragma unroll
+            for (int l = 0; l < LG; l++) {
+                const v4i fb = *(const v4i*)(st + (2 * RT * WP + 2 * (l * TTWG + wt) + sub) * FRAG);
+#pragma unroll
+                for (int i = 0; i < G::RI; i++)
+#pragma unroll
+                    for (int p = 0; p < WP; p++)
+                        acc[i][p + l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(fa[i][p], fb, acc[i][p + l], 0, 0, 0);
+            }
+        }
+    }
+    lds_barrier();
+}
+
+template <int WP, int LG>
+__device__ __forceinline__ void fold_pass(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0) {
+    using G = FoldShape<WP, LG>;
+    v16i acc[G::RI][G::NS];
+#pragma unroll
+    for (int i = 0; i < G::RI; i++)
+#pragma unroll
+        for (int s = 0; s < G::NS; s++) acc[i][s] = v16i{};
+    fold_mainloop<G, WP, LG>(a, smem, rt0, tt0, acc);
+    const uint32_t lane = threadIdx.x & 63, wr = (threadIdx.x >> 6) % 2;
+    const Q8View& w = a.w;
+    park_and_store<G, 1>(a, smem, rt0, tt0, [&](int i, int, int32_t (&v)[16]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+            const uint32_t row = rt0 * 32 + (wr * G::RI + i) * 32 + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+            dn::i128 tot = 0;
+#pragma unroll
+            for (int s = 0; s < G::NS; s++) tot += (dn::i128)((dn::u128)(dn::i128)acc[i][s][e] << (8 * s));
+            v[e] = row < w.rows ? dn::round_to_i32((dn::i128)((dn::u128)tot << w.fold_shift[row]), 24) : 0;
+        }
+    });
+}
+
+// 128 folded weight rows (64 for four planes) x 64 tokens per workgroup, blocks ordered as in
+// q8_gemm_row_kernel (contiguous ranges per XCD, bands of 8 row groups).
+template <int WP>
+__global__ __launch_bounds__(256, 1) void q8_gemm_fold_kernel(const GemvArgs a) {
+    __shared__ __attribute__((aligned(1024))) int8_t smem[FoldShape<WP, 5>::SMEM > FoldShape<WP, 3>::SMEM
+                                                                ? FoldShape<WP, 5>::SMEM
+                                                                : FoldShape<WP, 3>::SMEM];
+    int& s_limbs = *(int*)smem;
+    const uint32_t tid = threadIdx.x;
+    const uint32_t TT = (a.tokens + 31) / 32;
+    constexpr uint32_t RT = FoldShape<WP, 3>::RT, TG = 2;  // 32-row tiles, 32-token tiles per workgroup
+    const uint32_t n_rg = (a.w.tiles + 2 * RT - 1) / (2 * RT), n_tg = (TT + TG - 1) / TG;
+    const uint32_t total = n_rg * n_tg;
+    uint32_t b = blockIdx.x;
+    if (total % 8 == 0) b = (b % 8) * (total / 8) + b / 8;
+    const uint32_t band = b / (GM_BAND * n_tg), first = band * GM_BAND, rows_in_band = min(GM_BAND, n_rg - first);
+    const uint32_t r = b - band * GM_BAND * n_tg;
+    const uint32_t rt0 = (first + r % rows_in_band) * RT, tt0 = (r / rows_in_band) * TG;
+    if (tid == 0) s_limbs = 1;
+    __syncthreads();
+    if (tid < TG * 32 && tt0 * 32 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 32 + tid]);
+    __syncthreads();
+    const int limbs = s_limbs;
+    __syncthreads();
+    switch (limbs) {
+        case 1: fold_pass<WP, 1>(a, smem, rt0, tt0); break;
+        case 2: fold_pass<WP, 2>(a, smem, rt0, tt0); break;
+        case 3: fold_pass<WP, 3>(a, smem, rt0, tt0); break;
+        case 4: fold_pass<WP, 4>(a, smem, rt0, tt0); break;
+        default: fold_pass<WP, 5>(a, smem, rt0, tt0); break;
+    }
+}
+
 }  // namespace
 
 bool iris_gemm_applies(const GemvArgs& a) {
-    return a.planes && a.token_limbs && a.tokens >= 2 && a.w.scale_mode == Q8_SCALE_ROW && a.w.cols % 64 == 0 &&
-           a.w.cols < (1u << 17) && a.epilogue != EPI_HEAD_SELECT;
+    if (!a.planes || !a.token_limbs || a.tokens < 2 || a.w.cols % 64 || a.epilogue == EPI_HEAD_SELECT) return false;
+    if (a.w.scale_mode == Q8_SCALE_ROW) return a.w.cols < (1u << 17);
+    // Folded per-block scales: shared-shift sums stay below 2^31.
+    return a.w.scale_mode == Q8_SCALE_F16 && a.w.fold_planes && a.w.fold_nplanes >= 1 &&
+           a.w.fold_nplanes <= Q8_FOLD_MAX_PLANES && a.w.cols <= 16384;
 }
 
 int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
@@ -403,6 +662,18 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(digit_planes_kernel, dim3(TT, (KB + PLANE_KB - 1) / PLANE_KB), dim3(256), 0, stream, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return (int)st;
+    if (a.w.scale_mode == Q8_SCALE_F16) {
+        // 32-row tiles per workgroup: 4, or 2 for four planes (FoldShape::RT).
+        const uint32_t rt = a.w.fold_nplanes <= 3 ? 4 : 2;
+        const uint32_t n = (a.w.tiles + 2 * rt - 1) / (2 * rt) * ((TT + 1) / 2);
+        switch (a.w.fold_nplanes) {
+            case 1: hipLaunchKernelGGL(q8_gemm_fold_kernel<1>, dim3(n), dim3(256), 0, stream, a); break;
+            case 2: hipLaunchKernelGGL(q8_gemm_fold_kernel<2>, dim3(n), dim3(256), 0, stream, a); break;
+            case 3: hipLaunchKernelGGL(q8_gemm_fold_kernel<3>, dim3(n), dim3(256), 0, stream, a); break;
+            default: hipLaunchKernelGGL(q8_gemm_fold_kernel<4>, dim3(n), dim3(256), 0, stream, a); break;
+        }
+        return (int)hipGetLastError();
+    }
     // Two waves per SIMD and 256 rows when that still gives every CU a
     // workgroup, else one wave per SIMD and 128 rows.
     const uint32_t n_tg = (TT + GM_TT - 1) / GM_TT;
@@ -412,4 +683,47 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     else
         hipLaunchKernelGGL(q8_gemm_row_kernel<4>, dim3(n4), dim3(256), 0, stream, a);
     return (int)hipGetLastError();
+}
+
+int iris_q8_prepare_fold(Q8GpuMatrix* m, hipStream_t stream) {
+    static std::mutex lock;  // a matrix is folded once, whichever thread gets there first
+    std::lock_guard<std::mutex> guard(lock);
+    if (!m || m->fold_tried || m->scale_mode != Q8_SCALE_F16 || !m->sc16 || m->cols % 64) return 0;
+    m->fold_tried = true;
+    const size_t plane_bytes = (size_t)m->tiles * m->nb * Q8_TILE_BLOCK_BYTES;
+    int* d_need = nullptr;
+    int need = 0;
+    hipError_t st = hipMalloc((void**)&m->fold.shift, (size_t)m->tiles * Q8_TILE_ROWS * sizeof(int32_t));
+    if (st == hipSuccess) st = hipMalloc((void**)&d_need, sizeof(int));
+    if (st == hipSuccess) st = hipMemsetAsync(m->fold.shift, 0, (size_t)m->tiles * Q8_TILE_ROWS * sizeof(int32_t), stream);
+    if (st == hipSuccess) st = hipMemsetAsync(d_need, 0, sizeof(int), stream);
+    if (st == hipSuccess) {
+        hipLaunchKernelGGL(fold_rows_kernel, dim3((m->rows + 255) / 256), dim3(256), 0, stream, m->qs, m->sc16, m->rows,
+                           m->nb, m->fold.shift, d_need);
+        st = hipGetLastError();
+    }
+    if (st == hipSuccess) st = hipMemcpyAsync(&need, d_need, sizeof(int), hipMemcpyDeviceToHost, stream);
+    if (st == hipSuccess) st = hipStreamSynchronize(stream);
+    hipFree(d_need);
+    if (st == hipSuccess && need >= 1 && need <= (int)Q8_FOLD_MAX_PLANES) {
+        // Rows past the matrix in its last tile keep zero weights in every plane.
+        st = hipMalloc((void**)&m->fold.planes, plane_bytes * need);
+        if (st == hipSuccess) st = hipMemsetAsync(m->fold.planes, 0, plane_bytes * need, stream);
+        const size_t n = (size_t)m->rows * m->nb;
+        if (st == hipSuccess && n) {
+            hipLaunchKernelGGL(fold_planes_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, stream, m->qs,
+                               m->sc16, m->rows, m->nb, m->fold.shift, (uint32_t)need, plane_bytes, m->fold.planes);
+            st = hipGetLastError();
+        }
+        if (st == hipSuccess) st = hipStreamSynchronize(stream);
+        if (st == hipSuccess) {
+            m->fold.nplanes = (uint32_t)need;
+            m->device_bytes += plane_bytes * need + (size_t)m->tiles * Q8_TILE_ROWS * sizeof(int32_t);
+            return 0;
+        }
+    }
+    hipFree(m->fold.planes);
+    hipFree(m->fold.shift);
+    m->fold = Q8Folded{};
+    return (int)st;
 }

@@ -30,6 +30,20 @@ enum Q8ScaleMode : int {
 constexpr int Q8_TILE_ROWS = 16;
 constexpr int Q8_TILE_BLOCK_BYTES = 512;
 
+// Per-block f16 scales folded into the weights for the matrix cores: with
+// s_b = sign_b * m_b * 2^sh_b the Q.24 value of block b's scale (m_b < 2^11)
+// and R the least sh_b of the row, the integers w' = q * sign_b * (m_b <<
+// (sh_b - R)) give dot_row's total as 2^R * sum_k w'_k x_k. Each w' is kept
+// as `planes` signed byte digits (the activations' digit scheme), each
+// plane in the qs tile layout; `shift` holds R per row.
+struct Q8Folded {
+    int8_t* planes;    // [planes][tiles][nb][512]
+    int32_t* shift;    // [tiles * 16]
+    uint32_t nplanes;  // 0 = not prepared (or the spread of a row's scales is too wide)
+};
+
+constexpr uint32_t Q8_FOLD_MAX_PLANES = 4;
+
 struct Q8GpuMatrix {
     uint32_t rows, cols, nb, tiles;
     int scale_mode;
@@ -38,6 +52,8 @@ struct Q8GpuMatrix {
     int64_t* sc64;
     int64_t* row_scale;
     uint64_t device_bytes;
+    Q8Folded fold;
+    bool fold_tried;  // the folding was attempted (prepared or refused)
 };
 
 // Kernel-side view of a matrix.
@@ -48,11 +64,21 @@ struct Q8View {
     const int64_t* row_scale;
     uint32_t rows, cols, nb, tiles;
     int scale_mode;
+    const int8_t* fold_planes;
+    const int32_t* fold_shift;
+    uint32_t fold_nplanes;
 };
 
 inline Q8View q8_view(const Q8GpuMatrix* m) {
-    return Q8View{m->qs, m->sc16, m->sc64, m->row_scale, m->rows, m->cols, m->nb, m->tiles, m->scale_mode};
+    return Q8View{m->qs,   m->sc16,       m->sc64,       m->row_scale,      m->rows,        m->cols,
+                  m->nb,   m->tiles,      m->scale_mode, m->fold.planes,    m->fold.shift,  m->fold.nplanes};
 }
+
+// Builds m's folded planes (once; per-block scale matrices only) so that
+// multi-token products of it run on the matrix cores. Allocates device
+// memory. Leaves m unfolded, and returns 0, when a row's scales spread over
+// too many binary orders for Q8_FOLD_MAX_PLANES digits.
+int iris_q8_prepare_fold(Q8GpuMatrix* m, hipStream_t stream);
 
 // Prologue applied to the activations while they are staged.
 enum GemvPrologue : int {

@@ -897,6 +897,10 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
     if (max_rows > 1) {
+        // Per-block scale matrices go through the matrix cores folded.
+        for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++)
+            for (Q8GpuMatrix* w : {m->layers[l].wqkv, m->layers[l].wo, m->layers[l].wgu, m->layers[l].wdown})
+                if (st == hipSuccess) st = (hipError_t)iris_q8_prepare_fold(w, s->stream);
         size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
         if (st == hipSuccess) st = hipMalloc((void**)&s->planes, gemm_planes_bytes((uint32_t)widest, max_rows));
         alloc(&s->token_limbs, 2 * (size_t)max_rows);

@@ -48,14 +48,15 @@ def copy_calibration(mib: int = 256, repeats: int = 3) -> int:
     return n
 
 
-def time_gemv(iterations: int = 200, n: int = GEMV_N, k: int = GEMV_K) -> dict:
+def time_gemv(iterations: int = 200, n: int = GEMV_N, k: int = GEMV_K, per_row_scale: bool = True) -> dict:
     """Average duration of one Q8_0 GEMV launch (M=1) with one f16 scale per
-    row. Launches cycle through enough copies of the matrix (more than 600 MB
-    in all) that each reads its weights from HBM, not from the 256 MB
+    row (or per block: the device reads one f16 per block beside the
+    weights). Launches cycle through enough copies of the matrix (more than
+    600 MB in all) that each reads its weights from HBM, not from the 256 MB
     Infinity Cache."""
     from .tensor import Q8Matrix
 
-    raw = synth.q8_matrix(synth.tensor_seed(2, 1), n, k, synth.scale_base_for(k), True)
+    raw = synth.q8_matrix(synth.tensor_seed(2, 1), n, k, synth.scale_base_for(k), per_row_scale)
     copies = max(1, -(-600_000_000 // (n * k * 34 // 32)))
     mats = [Q8Matrix.from_bytes(raw, n, k) for _ in range(copies)]
     arr = (C.c_void_p * copies)(*[m.handle.value for m in mats])
@@ -76,15 +77,18 @@ INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 
 def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iterations: int = 20,
-              magnitude_bits: int = 21) -> dict:
+              magnitude_bits: int = 21, per_row_scale: bool = True) -> dict:
     """Average duration of one multi-token Q8_0 product on the int8 matrix
     cores (digit planes + MFMA GEMM) at the gate|up shape of the 2048-row
     pass, with activations of `magnitude_bits` bits (three signed byte
     digits for the default, as the normalised inputs of that pass have).
-    The matrix-core work is 2 * tokens * n * k per digit plane."""
+    The matrix-core work is 2 * tokens * n * k per digit plane of the
+    activations, times the weight digit planes of a per-block scale matrix
+    (its scales folded into the weights: one f16 per block, the reference
+    bundles' base + random significand layout)."""
     from .tensor import Q8Matrix
 
-    raw = synth.q8_matrix(synth.tensor_seed(3, 1), n, k, synth.scale_base_for(k), True)
+    raw = synth.q8_matrix(synth.tensor_seed(3, 1), n, k, synth.scale_base_for(k), per_row_scale)
     m = Q8Matrix.from_bytes(raw, n, k)
     rng = np.random.default_rng(4)
     half = 1 << (magnitude_bits - 1)
@@ -97,13 +101,19 @@ def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iteration
     ms = C.c_double()
     native.check(L.iris_time_product_ws(m.handle, dx.ptr, tokens, dout.ptr, ws.ptr, ws_bytes, iterations,
                                         C.byref(ms)), "time GEMM")
+    info = m.info()
     m.free()
     digits = 3 if magnitude_bits <= 24 else 4
-    ops = 2.0 * tokens * n * k * digits
+    # weight digit planes: 1 for a row-scale matrix; a folded one holds
+    # (device bytes - int8 weights - f16 scales - row shifts) / int8 weights
+    qs = n * k
+    wplanes = 1 if per_row_scale else round((info["bytes"] - qs - n * k // 32 * 2 - 4 * ((n + 15) // 16 * 16)) / qs)
+    ops = 2.0 * tokens * n * k * digits * wplanes
     tops = ops / (ms.value * 1e-3) / 1e12
-    return {"shape": f"M={tokens} K={k} N={n}", "us": round(ms.value * 1e3, 1), "digit_planes": digits,
+    return {"shape": f"M={tokens} K={k} N={n}", "scales": "per row" if per_row_scale else "per block (folded)",
+            "us": round(ms.value * 1e3, 1), "digit_planes": digits, "weight_planes": wplanes,
             "mfma_tops": round(tops, 1), "peak_tops": INT8_PEAK_TOPS, "frac": round(tops / INT8_PEAK_TOPS, 4),
-            "product_tops": round(tops / digits, 1)}
+            "product_tops": round(2.0 * tokens * n * k / (ms.value * 1e-3) / 1e12, 1)}
 
 
 def time_teacher_forced_session(dm, vocab: int, rows: int = 2048, repeats: int = 2) -> dict:
@@ -158,10 +168,10 @@ class DecodeBench:
         return MISTRAL_7B_WEIGHT_BYTES + 2 * 4 * kvw * s.num_hidden_layers * mean_ctx
 
 
-def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None) -> dict:
+def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None, per_row_scale: bool = True) -> dict:
     """time_teacher_forced_session on a freshly uploaded Mistral-7B-shape model."""
     log = log or (lambda msg: None)
-    model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
+    model = synth.mistral_7b(seed=MISTRAL_7B_SEED, per_row_scale=per_row_scale)
     dm = DeviceModel(model)
     vocab = model.vocab
     del model.tensors
@@ -195,6 +205,8 @@ def main(argv=None):
     ap.add_argument("--pass-rows", type=int, default=0,
                     help="time only the teacher-forced pass over this many rows")
     ap.add_argument("--gemm-only", action="store_true", help="time only the MFMA product at the gate|up shape")
+    ap.add_argument("--per-block", action="store_true",
+                    help="with --gemm-only, --gemv-only or --pass-rows: per-block scale matrices")
     ap.add_argument("--trace-decode", type=int, default=0, metavar="STEPS",
                     help="only a short decode of STEPS steps (for kernel traces)")
     args = ap.parse_args(argv)
@@ -203,16 +215,17 @@ def main(argv=None):
         print(json.dumps(trace_decode(args.trace_decode)), flush=True)
         return
     if args.gemm_only:
-        print(json.dumps(time_gemm()), flush=True)
+        print(json.dumps(time_gemm(per_row_scale=not args.per_block)), flush=True)
         return
     if args.pass_rows:
-        r = time_teacher_forced(args.pass_rows, log=lambda m: print(m, file=sys.stderr, flush=True))
+        r = time_teacher_forced(args.pass_rows, log=lambda m: print(m, file=sys.stderr, flush=True),
+                                per_row_scale=not args.per_block)
         print(json.dumps(r), flush=True)
         return
     if args.calibrate:
         copy_calibration()
     if args.gemv_only:
-        g = time_gemv()
+        g = time_gemv(per_row_scale=not args.per_block)
         print(json.dumps({"gemv_us": round(g["us"], 3), "gemv_copies": g["copies"],
                           "algorithmic_bytes": g["algorithmic_bytes"]}), flush=True)
         return

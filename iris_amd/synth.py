@@ -346,12 +346,15 @@ def gemma_2b(seed=0x2B2B) -> Model:
 MISTRAL_7B = dict(hidden=4096, layers=32, heads=32, kv_heads=8, head_dim=128, ffn=14336, vocab=32000)
 
 
-def mistral_7b(seed=0x7B7B, layers=32) -> Model:
+def mistral_7b(seed=0x7B7B, layers=32, per_row_scale=True) -> Model:
     """32 layers, hidden 4096, 32 heads of 128 with 8 KV heads, SwiGLU 14336,
-    vocab 32000, RoPE base 1e6, untied head."""
+    vocab 32000, RoPE base 1e6, untied head; one f16 scale per row, or per
+    block (``per_row_scale=False``: each block's own significand, the
+    reference bundles' layout)."""
     kw = dict(MISTRAL_7B)
     kw["layers"] = layers
-    return mistral_model(**kw, seed=seed, rope_base=1_000_000, eps=1e-5, max_positions=32768, tied_head=False)
+    return mistral_model(**kw, seed=seed, rope_base=1_000_000, eps=1e-5, max_positions=32768, tied_head=False,
+                         per_row_scale=per_row_scale)
 
 
 def token_ids(seed: int, count: int, vocab: int) -> np.ndarray:

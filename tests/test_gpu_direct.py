@@ -267,3 +267,22 @@ def test_upload_cache_by_mapped_key(tmp_path):
     assert cache.uploads == len(names)
     cache.clear()
     mapped.close()
+
+
+def test_per_block_teacher_forced_pass_matches_oracle():
+    # Per-block scale matrices (the reference bundles' layout) in a multi-row
+    # pass: every product runs folded on the matrix cores (q|k|v with the
+    # RoPE/KV epilogue, SwiGLU pairs, residuals); every layer's rows and
+    # hashes against the oracle.
+    m = synth.mistral_model(512, 2, 8, 2, 64, 1024, 2048, seed=23, per_row_scale=False)
+    ids = synth.token_ids(8, 300, 2048)
+    dm = DeviceModel(m)
+    s = Session(dm, 300, 300)
+    rows, hashes = s.layer_pass(ids)
+    r = cpu.OracleRun(m, 300)
+    _, layers = r.pass_rows(list(ids), 0, keep_layers=True)
+    for layer in range(m.num_layers):
+        assert np.array_equal(rows[layer], layers[layer]), layer
+        assert hashes[layer] == hashlib.sha256(layers[layer].astype("<i4").tobytes()).hexdigest()
+    s.free()
+    dm.free()

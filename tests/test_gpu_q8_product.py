@@ -245,3 +245,81 @@ def test_mfma_product_wide_row_scales():
     x = np.concatenate([rand_activations(rng, 1, cols, int(b)) for b in np.linspace(8, 32, tokens).astype(int)])
     got = product_ws(m, x)
     assert np.array_equal(got, cpu.linear_q8(x, raw))
+
+
+def per_block_matrix(rng, rows, cols, kind):
+    """Q8_0 rows with one f16 scale per block, both signs, every weight
+    byte: `kind` sets how the scales of a row spread (so how many digit
+    planes the folded weights need): "tiny" subnormal scales below 2^-17
+    (one or two planes), "same" one exponent per row with random
+    significands (three), "unit" scales of 0 or 2^-24 (one plane),
+    "spread4" exponents within 4 binary orders
+    (three), "spread12" within 12 (four), "wide" over 20 orders (not
+    foldable: the vector path), "top" exponents 26..30 (results saturate),
+    plus zero scales and all-zero rows."""
+    nb = cols // 32
+    base = rng.integers(1, 17, (rows, 1))
+    if kind == "tiny":
+        e = np.zeros((rows, nb), np.int64)
+        mant = rng.integers(0, 96, (rows, nb))
+    elif kind == "unit":
+        e = np.zeros((rows, nb), np.int64)
+        mant = rng.integers(0, 2, (rows, nb))
+    else:
+        spread = {"same": 0, "spread4": 4, "spread12": 12, "wide": 20, "top": 4}[kind]
+        lo = rng.integers(26, 27, (rows, 1)) if kind == "top" else base
+        e = lo + rng.integers(0, spread + 1, (rows, nb))
+        mant = rng.integers(0, 1024, (rows, nb))
+    bits = (rng.integers(0, 2, (rows, nb)) << 15) | (np.minimum(e, 30) << 10) | mant
+    bits[rng.random((rows, nb)) < 0.02] = 0  # zero scales
+    bits[::37] = 0                           # all-zero rows
+    raw = np.empty((rows, nb, 34), np.uint8)
+    raw[:, :, 0] = bits & 0xFF
+    raw[:, :, 1] = bits >> 8
+    raw[:, :, 2:] = rng.integers(0, 256, (rows, nb, 32))
+    return raw.reshape(rows, -1)
+
+
+@pytest.mark.parametrize("kind,folds", [("unit", True), ("tiny", True), ("same", True), ("spread4", True),
+                                        ("spread12", True), ("wide", False), ("top", True)])
+@pytest.mark.parametrize("tokens,rows,cols", [(603, 200, 128), (129, 136, 4160)])
+def test_per_block_scales_on_the_matrix_cores(kind, folds, tokens, rows, cols):
+    # Per-block scale matrices folded into weight digit planes for the int8
+    # matrix cores (or, when a row's scales spread too wide, left to the
+    # vector path): every digit count of the activations (token groups of
+    # 1..5 digits), partial row and token tiles, every output against the
+    # oracle's dot_row.
+    rng = np.random.default_rng(tokens + rows + len(kind))
+    raw = per_block_matrix(rng, rows, cols, kind)
+    m = Q8Matrix.from_bytes(raw, rows, cols)
+    assert m.info()["scale_mode"] == "f16"
+    before = m.info()["bytes"]
+    x = grouped_activations(rng, tokens, cols)
+    got = product_ws(m, x)
+    assert (m.info()["bytes"] > before) == folds  # the folded planes were built
+    assert np.array_equal(got, cpu.linear_q8(x, raw))
+    # again, from the folded planes already there
+    x2 = rand_activations(rng, 70, cols, 24)
+    assert np.array_equal(product_ws(m, x2), cpu.linear_q8(x2, raw))
+    # the no-allocation entry point gives the same values
+    L = native.lib()
+    dx = native.DeviceBuffer.from_array(x2)
+    dout = native.DeviceBuffer(70 * rows * 4)
+    native.check(L.q8gpu_product_device_noalloc(m.handle, dx.ptr, 70, dout.ptr, None), "noalloc")
+    native.check(L.q8gpu_synchronize(), "sync")
+    assert np.array_equal(dout.to_array(np.int32, (70, rows)), cpu.linear_q8(x2, raw))
+
+
+def test_per_block_gemm_at_the_benchmark_shape_sampled():
+    # The gate|up shape of the 2048-row pass with per-block scales (the
+    # reference bundles' layout: base + next % 64 significands, generate.py:59):
+    # sampled rows of every token against the oracle.
+    rows, cols, tokens = 28672, 4096, 2048
+    raw = synth.q8_matrix(synth.tensor_seed(12, 1), rows, cols, synth.scale_base_for(cols), False)
+    m = Q8Matrix.from_bytes(raw, rows, cols)
+    assert m.info()["scale_mode"] == "f16"
+    rng = np.random.default_rng(12)
+    x = rng.integers(-(1 << 20), 1 << 20, (tokens, cols)).astype(np.int32)
+    got = product_ws(m, x)
+    sel = np.sort(rng.choice(rows, 96, replace=False))
+    assert np.array_equal(got[:, sel], cpu.linear_q8(x, raw[sel]))
