@@ -64,11 +64,18 @@ def gemv_roofline(decode_timing):
 
 
 def cpu_baseline(model, threads, steps=4):
-    """The oracle's decode steps at positions 512.. with a random-filled KV
-    cache (the 512-token prompt pass is not run on the CPU). The oracle is
-    loaded here, after every GPU measurement."""
+    """The oracle (a C restatement of the reference's CPU kernels, OpenMP
+    over rows as the reference's rayon is) on this host, after every GPU
+    measurement, on bounded samples of each workload:
+    - decode: `steps` steps at positions 512.. over a random-filled KV cache
+      (the 512-token prompt pass is not run), on `threads` threads, and one
+      step on one thread;
+    - the two products of the microbenchmark: the M=1 GEMV (K=4096,
+      N=14336, row scales) and the M=512 GEMM (K=N=4096), on `threads`;
+    - the teacher-forced pass: one layer over the first 256 of the 2048 rows
+      (positions 0..255), reported in rows per second."""
     from oracle import cpu
-    run = cpu.OracleRun(model, PROMPT + steps + 1, threads=threads)
+    run = cpu.OracleRun(model, PROMPT + steps + 2, threads=threads)
     rng = np.random.default_rng(5)
     for layer in range(model.num_layers):
         run.k_cache[layer][:PROMPT] = rng.integers(-(1 << 18), 1 << 18, run.k_cache[layer][:PROMPT].shape)
@@ -80,9 +87,51 @@ def cpu_baseline(model, threads, steps=4):
         logits = run.logits(rows[-1])
         tok = int(np.argmax(logits))
     dt = time.perf_counter() - t0
+    # one step on one thread
+    run.threads = 1
+    t0 = time.perf_counter()
+    rows, _ = run.pass_rows([tok], PROMPT + steps)
+    run.logits(rows[-1])
+    dt1 = time.perf_counter() - t0
+    run.threads = threads
+
+    from iris_amd import synth
+    k, n = 4096, 14336
+    w = synth.q8_matrix(synth.tensor_seed(2, 1), n, k, synth.scale_base_for(k), True)
+    x1 = rng.integers(-127, 128, (1, k)).astype(np.int32) * 300
+    cpu.linear_q8(x1, w, threads)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        cpu.linear_q8(x1, w, threads)
+    gemv_us = (time.perf_counter() - t0) / 5 * 1e6
+    w2 = synth.q8_matrix(synth.tensor_seed(4, 1), 4096, 4096, synth.scale_base_for(4096), True)
+    x2 = rng.integers(-(1 << 20), 1 << 20, (512, 4096)).astype(np.int32)
+    t0 = time.perf_counter()
+    cpu.linear_q8(x2, w2, threads)
+    gemm_us = (time.perf_counter() - t0) * 1e6
+
+    tf_rows = 256
+    tf = cpu.OracleRun(model, tf_rows, threads=threads)
+    from iris_amd import decode_timing
+    ids = synth.token_ids(decode_timing.PROMPT_SEED, tf_rows, model.vocab)
+    x = tf.embed(list(ids))
+    t0 = time.perf_counter()
+    tf.layer_pass(0, x, 0)
+    tf_s = time.perf_counter() - t0
     return {"value": round(steps / dt, 4), "unit": "tokens/s", "cores": threads, "kind": "port",
             "sample": f"{steps} decode steps of the same model at positions {PROMPT}..{PROMPT + steps - 1} "
-                      f"over a random-filled KV cache (CPU oracle, {threads} threads; prompt pass not run)"}
+                      f"over a random-filled KV cache (CPU oracle, {threads} threads; prompt pass not run)",
+            "single_thread": {"value": round(1.0 / dt1, 4), "unit": "tokens/s", "cores": 1,
+                              "sample": f"one decode step at position {PROMPT + steps}"},
+            "gemv_us": {"value": round(gemv_us, 1), "cores": threads,
+                        "sample": "Q8_0 GEMV M=1 K=4096 N=14336 (row scales), mean of 5"},
+            "gemm_us": {"value": round(gemm_us, 1), "cores": threads,
+                        "sample": "Q8_0 GEMM M=512 K=4096 N=4096 (row scales), one product"},
+            "teacher_forced_layer": {"value": round(tf_rows / tf_s, 1), "unit": "rows/s", "cores": threads,
+                                     "ms_per_layer_2048_rows_linear": round(tf_s * 1e3 * 2048 / tf_rows, 1),
+                                     "sample": f"layer 0 over rows 0..{tf_rows - 1} of the 2048-row pass "
+                                               "(attention grows with the rows, so 2048 rows take longer "
+                                               "than the linear figure)"}}
 
 
 def main():
@@ -142,11 +191,26 @@ def main():
     log(f"MFMA GEMM per-block scales {gemm_pb['shape']}: {gemm_pb['us']} us, {gemm_pb['weight_planes']} weight planes "
         f"= {gemm_pb['mfma_tops']} TOP/s ({100 * gemm_pb['frac']:.1f}% of int8 peak)")
 
+    # The Gemma-2B-shape decode (a 128-token prompt, then 255 timed steps).
+    gb = decode_timing.GemmaDecodeBench(255, log=log)
+    gb.run(8)
+    g_ms, g_pre, _ = gb.run(255)
+    g_bytes = gb.bytes_per_step(255)
+    gb.free()
+    g_gbps = g_bytes / (g_ms * 1e-3) / 1e9
+    gemma = {"workload": "gemma-2b-shape Q8_0 greedy decode, prompt 128 + 256 tokens, batch 1",
+             "tokens_per_s": round(1e3 / g_ms, 2), "ms_per_step": round(g_ms, 4), "prompt_pass_ms": round(g_pre, 2),
+             "bytes_per_token": int(g_bytes), "achieved": round(g_gbps, 1), "unit": "GB/s",
+             "frac": round(g_gbps / PEAK_HBM_GBPS, 4)}
+    log(f"gemma-2b decode {g_ms:.3f} ms/token ({gemma['tokens_per_s']} tokens/s, {g_gbps:.0f} GB/s)")
+
     base = None
     if not args.no_cpu:
         threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
         base = cpu_baseline(synth.mistral_7b(seed=decode_timing.MISTRAL_7B_SEED), threads, args.cpu_steps)
-        log(f"CPU oracle: {base['value']} tokens/s on {threads} threads")
+        log(f"CPU oracle: {base['value']} tokens/s on {threads} threads, {base['single_thread']['value']} on 1; "
+            f"GEMV {base['gemv_us']['value']} us, GEMM M=512 {base['gemm_us']['value']} us; "
+            f"teacher-forced layer {base['teacher_forced_layer']['value']} rows/s")
 
     line = {
         "metric": METRIC, "value": round(1000.0 / ms_per_token, 2), "unit": "tokens/s", "n_gpus": 1,
@@ -161,6 +225,7 @@ def main():
                             "unit": "GB/s", "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
                             "bytes_per_token": int(per_token)},
         "prompt_pass_ms": round(prefill_ms, 2),
+        "gemma_2b_decode": gemma,
         "deterministic_rerun": deterministic,
         "teacher_forced": dict(tf, workload="mistral-7b-shape chain pass over 2048 uniform ids, "
                                             "per-layer SHA-256 checkpoints", mfma_gemm=gemm,

@@ -168,6 +168,65 @@ class DecodeBench:
         return MISTRAL_7B_WEIGHT_BYTES + 2 * 4 * kvw * s.num_hidden_layers * mean_ctx
 
 
+GEMMA_2B_SEED = 0x2B2B
+GEMMA_PROMPT = 128
+
+
+def decode_step_bytes(model) -> int:
+    """Bytes of weights one decode step reads, from the model's tensors: every
+    layer matrix and the head as Q8_0 (34 bytes per 32 weights), the Q16.16
+    matrices (PLE gate and projection, the per-layer model projection) at 4
+    bytes a value, and one embedding row per table (the selected token's)."""
+    from .model import PREFIX
+    total = 0
+    for name, t in model.tensors.items():
+        if not name.startswith(PREFIX + "layers.") and name not in (PREFIX + "lm_head.weight",
+                                                                    PREFIX + "per_layer_model_projection.weight"):
+            continue
+        total += t.nbytes
+    if model.shape.tied_head:
+        total += model.tensors[PREFIX + "embed_tokens.weight"].nbytes
+    for table in (PREFIX + "embed_tokens.weight", PREFIX + "embed_tokens_per_layer.weight"):
+        if table in model.tensors:
+            total += model.tensors[table].shape[1]
+    return int(total)
+
+
+class GemmaDecodeBench:
+    """The Gemma-2B-shape model (18 layers, hidden 2048, 8 heads of 256 on
+    one KV head, GeGLU 16384, vocab 256000, PLE 256, softcap 30, tied head)
+    on the device, a 128-token prompt and `max_steps` decode steps."""
+
+    def __init__(self, max_steps: int, log=None):
+        import time
+        log = log or (lambda msg: None)
+        t = time.time()
+        model = synth.gemma_2b(seed=GEMMA_2B_SEED)
+        log(f"gemma-2b weights generated in {time.time() - t:.1f}s")
+        self.weight_bytes = decode_step_bytes(model)
+        self.dm = DeviceModel(model)
+        self.shape = model.shape
+        self.layers = model.num_layers
+        self.head_dims = [model.head_dim_at(layer) for layer in range(model.num_layers)]
+        del model.tensors
+        self.session = Session(self.dm, GEMMA_PROMPT + max_steps + 1, GEMMA_PROMPT)
+        self.prompt = synth.token_ids(PROMPT_SEED, GEMMA_PROMPT, self.shape.vocab_size)
+
+    def run(self, steps: int):
+        return self.session.time_decode(self.prompt, steps)
+
+    def bytes_per_step(self, steps: int) -> float:
+        """Weights (decode_step_bytes) plus every layer's K and V up to the
+        step's position, averaged over the run."""
+        mean_ctx = GEMMA_PROMPT + (steps + 1) / 2.0
+        kv = sum(2 * 4 * self.shape.num_key_value_heads * hd for hd in self.head_dims)
+        return self.weight_bytes + kv * mean_ctx
+
+    def free(self):
+        self.session.free()
+        self.dm.free()
+
+
 def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None, per_row_scale: bool = True) -> dict:
     """time_teacher_forced_session on a freshly uploaded Mistral-7B-shape model."""
     log = log or (lambda msg: None)
@@ -209,10 +268,22 @@ def main(argv=None):
                     help="with --gemm-only, --gemv-only or --pass-rows: per-block scale matrices")
     ap.add_argument("--trace-decode", type=int, default=0, metavar="STEPS",
                     help="only a short decode of STEPS steps (for kernel traces)")
+    ap.add_argument("--gemma-2b", type=int, default=0, metavar="STEPS",
+                    help="only the Gemma-2B-shape decode: a 128-token prompt and STEPS timed steps")
     args = ap.parse_args(argv)
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
     if args.trace_decode:
         print(json.dumps(trace_decode(args.trace_decode)), flush=True)
+        return
+    if args.gemma_2b:
+        g = GemmaDecodeBench(args.gemma_2b, log=lambda m: print(m, file=sys.stderr, flush=True))
+        g.run(8)
+        ms, prefill, _ = g.run(args.gemma_2b)
+        b = g.bytes_per_step(args.gemma_2b)
+        print(json.dumps({"decode_ms_per_step": round(ms, 4), "tokens_per_s": round(1e3 / ms, 1),
+                          "prompt_pass_ms": round(prefill, 2), "bytes_per_step": int(b),
+                          "achieved_gbps": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
+        g.free()
         return
     if args.gemm_only:
         print(json.dumps(time_gemm(per_row_scale=not args.per_block)), flush=True)
