@@ -107,27 +107,61 @@ __global__ __launch_bounds__(NT) void norm_residual_kernel(const int32_t* a, uin
 // out[t][r] = requantize(wrapping sum_k x[t][k] * W[r][k]) for a Q16.16
 // matrix W [rows][cols] (dot_bits, tensor.rs:522-528; mac_bits ops.rs:17-19),
 // optionally followed by mul_sat(gelu(.), aux[t][r]) (the PLE gate,
-// prefill_range.rs:931-944). One row per wave, four rows per workgroup.
-__global__ __launch_bounds__(NT) void i32_gemv_kernel(const I32GemvArgs a) {
+// prefill_range.rs:931-944). Four waves per workgroup, rows_per_wave rows
+// each (row = base + j * NW + wave).
+//
+// One-row extras (I32GemvArgs): the input formed in LDS as the post-norm
+// and residual of the previous product (norm_residual_kernel's arithmetic),
+// and per-workgroup sums of squares of the outputs.
+__global__ __launch_bounds__(NT) void i32_gemv_kernel(const I32GemvArgs a, uint32_t rows_per_wave) {
+    extern __shared__ __align__(16) int32_t s_x[];  // the staged input row (res_in set)
+    __shared__ int64_t s_red[NW];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const uint32_t row = blockIdx.x * NW + wave, t = blockIdx.y;
-    if (row >= a.rows) return;
+    const uint32_t t = blockIdx.y;
     const int32_t* xr = a.x + (size_t)t * a.x_stride;
-    const int32_t* wr = a.w + (size_t)row * a.cols;
-    uint64_t acc = 0;
-    for (uint32_t k = lane * 4; k < a.cols; k += 256) {
-        const int4 xv = *(const int4*)(xr + k);
-        const int4 wv = *(const int4*)(wr + k);
-        acc += (uint64_t)((int64_t)xv.x * wv.x);
-        acc += (uint64_t)((int64_t)xv.y * wv.y);
-        acc += (uint64_t)((int64_t)xv.z * wv.z);
-        acc += (uint64_t)((int64_t)xv.w * wv.w);
+    if (a.res_in) {
+        int64_t ss = 0;
+        for (uint32_t i = lane; i < a.ssq_n; i += 64) ss = dn::acc_add_sat(ss, a.ssq_in[i]);
+        const int32_t scale = dn::rms_scale_from_sum(wave_sum_sat(ss), a.cols, a.eps);
+        const bool store = a.res_out != nullptr && blockIdx.x == 0;
+        for (uint32_t i = tid; i < a.cols; i += NT) {
+            const int32_t y = dn::add_sat(dn::mul_sat(dn::mul_sat(xr[i], scale), a.res_norm_w[i]), a.res_in[i]);
+            s_x[i] = y;
+            if (store) a.res_out[i] = y;
+        }
+        __syncthreads();
+        xr = s_x;
     }
-    for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
-    if (lane == 0) {
+    int64_t sq = 0;
+    const uint32_t base = blockIdx.x * NW * rows_per_wave;
+    for (uint32_t j = 0; j < rows_per_wave; j++) {
+        const uint32_t row = base + j * NW + wave;
+        if (row >= a.rows) break;
+        const int32_t* wr = a.w + (size_t)row * a.cols;
+        uint64_t acc = 0;
+        for (uint32_t k = lane * 4; k < a.cols; k += 256) {
+            const int4 xv = *(const int4*)(xr + k);
+            const int4 wv = *(const int4*)(wr + k);
+            acc += (uint64_t)((int64_t)xv.x * wv.x);
+            acc += (uint64_t)((int64_t)xv.y * wv.y);
+            acc += (uint64_t)((int64_t)xv.z * wv.z);
+            acc += (uint64_t)((int64_t)xv.w * wv.w);
+        }
+        for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
         int32_t v = dn::requantize((int64_t)acc);
         if (a.aux) v = dn::mul_sat(dn::gelu(v), a.aux[(size_t)t * a.aux_stride + row]);
-        a.out[(size_t)t * a.out_stride + row] = v;
+        if (lane == 0) a.out[(size_t)t * a.out_stride + row] = v;
+        sq = dn::acc_add_sat(sq, (int64_t)v * v);
+    }
+    if (a.ssq_out) {
+        // Every lane holds its wave's sum (the values are wave-uniform).
+        if (lane == 0) s_red[wave] = sq;
+        __syncthreads();
+        if (tid == 0) {
+            int64_t total = 0;
+            for (uint32_t i = 0; i < NW; i++) total = dn::acc_add_sat(total, s_red[i]);
+            a.ssq_out[blockIdx.x] = total;
+        }
     }
 }
 
@@ -194,10 +228,27 @@ int iris_norm_residual_launch(const int32_t* a, uint32_t a_stride, const int32_t
     return (int)hipGetLastError();
 }
 
+uint32_t i32_gemv_slots(uint32_t rows) {
+    const uint32_t per_wave = (rows + NW * I32_GEMV_MAX_SLOTS - 1) / (NW * I32_GEMV_MAX_SLOTS);
+    return (rows + NW * per_wave - 1) / (NW * per_wave);
+}
+
 int iris_i32_gemv_launch(const I32GemvArgs& a, uint32_t tokens, hipStream_t stream) {
     if (a.rows == 0 || a.cols == 0 || a.cols % 4 || a.x_stride % 4) return IRIS_E_INVALID;
     if (tokens == 0) return 0;
-    hipLaunchKernelGGL(i32_gemv_kernel, dim3((a.rows + NW - 1) / NW, tokens), dim3(NT), 0, stream, a);
+    if ((a.res_in || a.ssq_out) && tokens != 1) return IRIS_E_INVALID;
+    size_t shmem = 0;
+    if (a.res_in) {
+        if (!a.res_norm_w || !a.ssq_in || a.ssq_n == 0 || a.cols > I32_GEMV_MAX_STAGED) return IRIS_E_INVALID;
+        if (a.res_out && (a.res_out == a.res_in || a.res_out == a.x)) return IRIS_E_INVALID;
+        shmem = (size_t)a.cols * 4;
+    }
+    uint32_t per_wave = 1, wgs = (a.rows + NW - 1) / NW;
+    if (a.ssq_out) {
+        wgs = i32_gemv_slots(a.rows);
+        per_wave = (a.rows + NW * I32_GEMV_MAX_SLOTS - 1) / (NW * I32_GEMV_MAX_SLOTS);
+    }
+    hipLaunchKernelGGL(i32_gemv_kernel, dim3(wgs, tokens), dim3(NT), shmem, stream, a, per_wave);
     return (int)hipGetLastError();
 }
 

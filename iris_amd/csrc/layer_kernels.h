@@ -99,7 +99,27 @@ struct I32GemvArgs {
     uint32_t out_stride;
     const int32_t* aux;      // nullable: out = mul_sat(gelu(dot), aux[t][r])
     uint32_t aux_stride;
+    // One row (tokens == 1) only:
+    // - res_in set: the product's input is y = add_sat(rms_norm(x, res_norm_w, eps), res_in),
+    //   the norm's sum of squares from ssq_in[0 .. ssq_n); workgroup 0 writes y to res_out
+    //   (nullable; not x or res_in); cols <= I32_GEMV_MAX_STAGED;
+    // - ssq_out set: one saturating sum of squares of the outputs per workgroup,
+    //   ssq_out[0 .. i32_gemv_slots(rows)).
+    const int32_t* res_in;
+    const int32_t* res_norm_w;
+    int64_t eps;
+    const int64_t* ssq_in;
+    uint32_t ssq_n;
+    int32_t* res_out;
+    int64_t* ssq_out;
 };
+
+constexpr uint32_t I32_GEMV_MAX_STAGED = 8192;  // elements of a staged input row (32 KiB of LDS)
+constexpr uint32_t I32_GEMV_MAX_SLOTS = 256;
+// Workgroups (and sum-of-squares slots) of a one-row launch with ssq_out:
+// four waves, each taking rows_per_wave rows, so that at most
+// I32_GEMV_MAX_SLOTS workgroups cover the rows.
+uint32_t i32_gemv_slots(uint32_t rows);
 
 struct PleArgs {
     const int32_t* proj;     // [rows][row_stride]: dot_bits of the projection, all segments

@@ -646,7 +646,9 @@ __global__ __launch_bounds__(256, 1) void q8_gemm_fold_kernel(const GemvArgs a) 
 }  // namespace
 
 bool iris_gemm_applies(const GemvArgs& a) {
-    if (!a.planes || !a.token_limbs || a.tokens < 2 || a.w.cols % 64 || a.epilogue == EPI_HEAD_SELECT) return false;
+    if (!a.planes || !a.token_limbs || a.tokens < 2 || a.w.cols % 64 || a.epilogue == EPI_HEAD_SELECT ||
+        a.prologue == PRO_NORM_RES_NORM)
+        return false;
     if (a.w.scale_mode == Q8_SCALE_ROW) return a.w.cols < (1u << 17);
     // Folded per-block scales: shared-shift sums stay below 2^31.
     return a.w.scale_mode == Q8_SCALE_F16 && a.w.fold_planes && a.w.fold_nplanes >= 1 &&

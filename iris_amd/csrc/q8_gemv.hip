@@ -239,10 +239,10 @@ __device__ __forceinline__ void finish_tile(const GemvArgs& a, uint32_t tile, ui
         return;
     }
     if (a.ssq_out) {
-        // The tile's rows as stored (add_sat with the residual), squared and
-        // summed with saturation over the 16 lanes.
+        // The tile's rows as stored (add_sat with the residual, or as they
+        // are), squared and summed with saturation over the 16 lanes.
         const bool own = lane < Q8_TILE_ROWS && row < w.rows;
-        const int32_t o = dn::add_sat(v, in.epi.res);
+        const int32_t o = a.epilogue == EPI_RESIDUAL ? dn::add_sat(v, in.epi.res) : v;
         const int64_t sq = row16_sum_sat_nonneg(own ? (int64_t)o * o : 0);
         if (lane == 0) a.ssq_out[tile] = sq;
     }
@@ -299,6 +299,23 @@ __device__ __forceinline__ int stage_int4(int4 v, bool norm, int4 nw, int32_t sc
     return need;
 }
 
+// add_sat(mul_sat(mul_sat(v, scale), w), r), then mul_sat(., scalar) when
+// scalar is set: a post-norm with its residual and layer scalar.
+__device__ __forceinline__ int4 norm_res4(int4 v, int4 w, int4 r, int32_t scale, int32_t scalar) {
+    int4 y;
+    y.x = dn::add_sat(dn::mul_sat(dn::mul_sat(v.x, scale), w.x), r.x);
+    y.y = dn::add_sat(dn::mul_sat(dn::mul_sat(v.y, scale), w.y), r.y);
+    y.z = dn::add_sat(dn::mul_sat(dn::mul_sat(v.z, scale), w.z), r.z);
+    y.w = dn::add_sat(dn::mul_sat(dn::mul_sat(v.w, scale), w.w), r.w);
+    if (scalar != 0) {
+        y.x = dn::mul_sat(y.x, scalar);
+        y.y = dn::mul_sat(y.y, scalar);
+        y.z = dn::mul_sat(y.z, scalar);
+        y.w = dn::mul_sat(y.w, scalar);
+    }
+    return y;
+}
+
 __device__ __forceinline__ int64_t sumsq4(int64_t s, int4 v) {
     s = dn::acc_add_sat(s, (int64_t)v.x * v.x);
     s = dn::acc_add_sat(s, (int64_t)v.y * v.y);
@@ -307,6 +324,7 @@ __device__ __forceinline__ int64_t sumsq4(int64_t s, int4 v) {
 }
 
 constexpr uint32_t XROUND = 4;  // int4 loads a thread has in flight per staging round
+constexpr uint32_t NRN_ROUND = 2;  // int4 of the row per thread under PRO_NORM_RES_NORM
 
 // The persistent kernel's prologue: the row's rms_norm scale when asked
 // (sum of squares: saturating, non-negative terms, so order-free) and every
@@ -317,10 +335,16 @@ constexpr uint32_t XROUND = 4;  // int4 loads a thread has in flight per staging
 // issued: the weight loads it issues queue behind the row's, and only LDS
 // barriers follow, so they stay in flight through the staging. Returns the
 // digits the row needs.
-template <int NT, bool NORM, typename Issue>
+//
+// PRO_NORM_RES_NORM (a row of at most XROUND * NT dwords, the launcher's
+// check): the row is first y = norm_res4(x, res_norm_w, res_in) with the
+// scale from the producer's slots, then rms_norm'ed as above; workgroup 0
+// stores y.
+template <int NT, int PRO, typename Issue>
 __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes, int64_t* ssq,
                          uint32_t tid, Issue&& issue) {
     const uint32_t lane = tid & 63, wave = tid >> 6;
+    constexpr bool NORM = PRO != PRO_NONE;
     constexpr bool norm = NORM;
     const int4* x4 = (const int4*)x;
     const int4* n4 = (const int4*)a.norm_w;
@@ -361,6 +385,51 @@ __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, ui
         return dn::rms_scale_from_sum(t, pw * 4, a.norm_eps);
     };
     int4 v[XROUND], nw[XROUND];
+    constexpr uint32_t SPL = GEMV_SSQ_SLOTS / 64;
+    if constexpr (PRO == PRO_NORM_RES_NORM) {
+        // At most NRN_ROUND dwords per thread (the launcher's limit): x, its
+        // norm weights, the residual and both norms' weights in registers.
+        int4 xv[NRN_ROUND], wv[NRN_ROUND], rv[NRN_ROUND], mv[NRN_ROUND];
+        const int4* r4 = (const int4*)a.res_in;
+        const int4* rw4 = (const int4*)a.res_norm_w;
+#pragma unroll
+        for (uint32_t u = 0; u < NRN_ROUND; u++) xv[u] = x4[min(u * NT + tid, pw - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < NRN_ROUND; u++) rv[u] = r4[min(u * NT + tid, pw - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < NRN_ROUND; u++) wv[u] = rw4[min(u * NT + tid, pw - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < NRN_ROUND; u++) mv[u] = n4[min(u * NT + tid, pw - 1)];
+        int64_t sl[SPL];
+#pragma unroll
+        for (uint32_t u = 0; u < SPL; u++) sl[u] = a.ssq_in[min(lane + 64 * u, a.ssq_n - 1)];
+        __builtin_amdgcn_sched_barrier(0);
+        issue();
+        int64_t t = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < SPL; u++)
+            if (lane + 64 * u < a.ssq_n) t = dn::acc_add_sat(t, sl[u]);
+        const int32_t scale1 = dn::rms_scale_from_sum(wave_sum_sat_nonneg(t), pw * 4, a.norm_eps);
+        const bool store = a.res_out != nullptr && blockIdx.x == 0;
+        int64_t s = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < NRN_ROUND; u++) {
+            const uint32_t i = u * NT + tid;
+            xv[u] = norm_res4(xv[u], wv[u], rv[u], scale1, a.res_scalar);
+            if (i < pw) {
+                if (store) ((int4*)a.res_out)[i] = xv[u];
+                s = sumsq4(s, xv[u]);
+            }
+        }
+        const int32_t scale2 = finish_scale(s);
+        int need = 1;
+#pragma unroll
+        for (uint32_t u = 0; u < NRN_ROUND; u++) {
+            const uint32_t i = u * NT + tid;
+            if (i < pw) need = max(need, stage_int4(xv[u], true, mv[u], scale2, i, planes, pw));
+        }
+        return need;
+    }
     if (pw <= XROUND * NT) {
         load_round(0, v, nw);
         // The producer's per-tile sums of squares, when given: loaded with
@@ -368,7 +437,6 @@ __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, ui
         // summed by every wave on its own, so no barrier waits for the
         // slowest wave's row before the planes.
         const bool slots = norm && a.ssq_in != nullptr;
-        constexpr uint32_t SPL = GEMV_SSQ_SLOTS / 64;
         int64_t sl[SPL];
 #pragma unroll
         for (uint32_t u = 0; u < SPL; u++)
@@ -595,7 +663,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
 // W waves per workgroup: 8 (two workgroups per CU) for matrices with many
 // tiles, 16 (one per CU, the same 16 waves) when a matrix has at most one
 // tile per CU, so that its few tiles still keep every wave slot busy.
-template <int MODE, int W, bool NORM>
+template <int MODE, int W, int PRO>
 __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split) {
     extern __shared__ __align__(16) uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
     __shared__ dn::i128 red[W][Q8_TILE_ROWS];
@@ -644,7 +712,7 @@ __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a
     };
 
     // Once per workgroup: the norm scale and every digit plane of the row.
-    const int need = stage_row<W * 64, NORM>(a, x, pw, planes, ssq, tid, issue);
+    const int need = stage_row<W * 64, PRO>(a, x, pw, planes, ssq, tid, issue);
     const int wave_need = wave_max_int(need);
     if (lane == 0) s_need[wave] = wave_need;
     lds_barrier();
@@ -751,19 +819,14 @@ void gemv_prepare_once() {
         g_num_cus = prop.multiProcessorCount;
     if (g_num_cus <= 0) g_num_cus = 256;
     const int bytes = MAX_LIMBS * PERSISTENT_MAX_K;
-    for (const void* f : {(const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 8, false>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 8, false>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 8, false>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 16, false>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 16, false>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 16, false>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 8, true>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 8, true>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 8, true>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_ROW, 16, true>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_F16, 16, true>,
-                          (const void*)&q8_gemv_persistent<Q8_SCALE_I64, 16, true>})
+#define IRIS_PERSISTENT_W(M, P) (const void*)&q8_gemv_persistent<M, 8, P>, (const void*)&q8_gemv_persistent<M, 16, P>
+#define IRIS_PERSISTENT_P(P) \
+    IRIS_PERSISTENT_W(Q8_SCALE_ROW, P), IRIS_PERSISTENT_W(Q8_SCALE_F16, P), IRIS_PERSISTENT_W(Q8_SCALE_I64, P)
+    for (const void* f : {IRIS_PERSISTENT_P(PRO_NONE), IRIS_PERSISTENT_P(PRO_RMSNORM),
+                          IRIS_PERSISTENT_P(PRO_NORM_RES_NORM)})
         hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+#undef IRIS_PERSISTENT_P
+#undef IRIS_PERSISTENT_W
     if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
 }
 
@@ -804,18 +867,16 @@ int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) 
     const uint32_t wgs = min(groups, (uint32_t)resident);
     const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
     dim3 grid(wgs, a.tokens);
-    const bool norm = a.prologue == PRO_RMSNORM;
-    switch (a.w.scale_mode * 2 + (norm ? 1 : 0)) {
-#define IRIS_PERSISTENT(M, N)                                                                                   \
-    case M * 2 + N:                                                                                             \
-        hipLaunchKernelGGL((q8_gemv_persistent<M, W, N>), grid, dim3(W * 64), shmem, stream, a, split); \
+    switch (a.w.scale_mode * 3 + a.prologue) {
+#define IRIS_PERSISTENT(M, P)                                                                                   \
+    case M * 3 + P:                                                                                             \
+        hipLaunchKernelGGL((q8_gemv_persistent<M, W, P>), grid, dim3(W * 64), shmem, stream, a, split); \
         break;
-        IRIS_PERSISTENT(Q8_SCALE_ROW, false)
-        IRIS_PERSISTENT(Q8_SCALE_ROW, true)
-        IRIS_PERSISTENT(Q8_SCALE_F16, false)
-        IRIS_PERSISTENT(Q8_SCALE_F16, true)
-        IRIS_PERSISTENT(Q8_SCALE_I64, false)
-        IRIS_PERSISTENT(Q8_SCALE_I64, true)
+#define IRIS_PERSISTENT_M(M) IRIS_PERSISTENT(M, PRO_NONE) IRIS_PERSISTENT(M, PRO_RMSNORM) IRIS_PERSISTENT(M, PRO_NORM_RES_NORM)
+        IRIS_PERSISTENT_M(Q8_SCALE_ROW)
+        IRIS_PERSISTENT_M(Q8_SCALE_F16)
+        IRIS_PERSISTENT_M(Q8_SCALE_I64)
+#undef IRIS_PERSISTENT_M
 #undef IRIS_PERSISTENT
         default: return IRIS_E_INVALID;
     }
@@ -841,11 +902,21 @@ int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.tokens == 0 || a.w.rows == 0) return 0;
     if (iris_gemm_applies(a)) return iris_gemm_launch(a, stream);
     if (a.w.cols % 32 || a.x_stride % 4 || ((uintptr_t)a.x & 15)) return IRIS_E_INVALID;
-    if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
+    if (a.prologue < PRO_NONE || a.prologue > PRO_NORM_RES_NORM) return IRIS_E_INVALID;
+    if (a.prologue != PRO_NONE && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
     if (a.tokens > 65535) return IRIS_E_INVALID;
     if ((a.ssq_out || a.ssq_in) && a.tokens != 1) return IRIS_E_INVALID;
-    if (a.ssq_out && a.epilogue != EPI_RESIDUAL) return IRIS_E_INVALID;
-    if (a.ssq_in && (a.prologue != PRO_RMSNORM || a.ssq_n == 0 || a.ssq_n > GEMV_SSQ_SLOTS)) return IRIS_E_INVALID;
+    if (a.ssq_out && a.epilogue != EPI_RESIDUAL && a.epilogue != EPI_STORE) return IRIS_E_INVALID;
+    if (a.ssq_in && (a.prologue == PRO_NONE || a.ssq_n == 0 || a.ssq_n > GEMV_SSQ_SLOTS)) return IRIS_E_INVALID;
+    if (a.prologue == PRO_NORM_RES_NORM) {
+        // One row of at most NRN_ROUND dwords per thread of an 8-wave
+        // workgroup, staged from the producer's slots; y is written apart
+        // from every buffer the launch reads.
+        if (!a.ssq_in || a.tokens != 1 || a.w.cols > NRN_ROUND * 8 * 64 * 4) return IRIS_E_INVALID;
+        if (((uintptr_t)a.res_in & 15) || ((uintptr_t)a.res_norm_w & 15) || ((uintptr_t)a.res_out & 15))
+            return IRIS_E_INVALID;
+        if (a.res_out && (a.res_out == a.res_in || a.res_out == a.x)) return IRIS_E_INVALID;
+    }
     gemv_prepare_once();
     if (a.w.cols <= PERSISTENT_MAX_K) {
         // Long rows (K >= 8192) of a matrix with at most one tile per CU: one

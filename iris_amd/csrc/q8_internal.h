@@ -84,6 +84,13 @@ int iris_q8_prepare_fold(Q8GpuMatrix* m, hipStream_t stream);
 enum GemvPrologue : int {
     PRO_NONE = 0,
     PRO_RMSNORM = 1,  // rms_norm(x, norm_w, eps) (ops.rs:98-114), computed per workgroup
+    // One row (gemma-dense's post-norm, residual and layer scalar, then the
+    // next norm, prefill_range.rs:879-958): y = add_sat(rms_norm(x,
+    // res_norm_w), res_in), times res_scalar when set; the product takes
+    // rms_norm(y, norm_w). The first norm's sum of squares comes from the
+    // producer's tile slots (ssq_in); workgroup 0 writes y to res_out
+    // (nullable).
+    PRO_NORM_RES_NORM = 2,
 };
 
 // Epilogue applied to each finished output.
@@ -148,6 +155,11 @@ struct GemvArgs {
     int64_t* ssq_out;
     const int64_t* ssq_in;
     uint32_t ssq_n;
+    // PRO_NORM_RES_NORM
+    const int32_t* res_norm_w;
+    const int32_t* res_in;
+    int32_t res_scalar;         // 0 = none
+    int32_t* res_out;
 };
 
 constexpr uint32_t GEMV_SSQ_SLOTS = 256;

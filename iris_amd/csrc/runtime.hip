@@ -549,7 +549,8 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
 
 // One gemma-dense pass (crates/inference/kernels/src/prefill_range.rs:307-958
 // per layer, the PLE prepare of view_kernels.rs:59-99 first): eleven launches
-// per layer.
+// per layer, eight for one row.
+//
 // The PLE inputs of every layer (view_kernels.rs:59-99) from the embedded
 // rows in s->x and their ids, into s->ple_rows [rows][layers * ple_width].
 static int gemma_ple(IrisSession* s, uint32_t rows) {
@@ -584,15 +585,28 @@ static int gemma_ple(IrisSession* s, uint32_t rows) {
 
 // One gemma-dense layer over the rows in s->x (positions from *d_pos), with
 // the layer's PLE inputs in s->ple_rows; the output back in s->x.
-static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
+//
+// With `carry` (one row): no separate norm launches. The previous layer's
+// PLE post-norm, still carried, is formed in the q|k|v product's prologue;
+// the o and down products leave their row in tmp with per-tile sums of
+// squares, and the post-norm and residual are formed in the prologue of
+// the product after each (gate|up, the PLE gate); this layer's PLE
+// post-norm is left carried. The residual alternates between x and
+// attended (a prologue writes its row apart from the one it reads).
+static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     const uint32_t H = d.hidden, P = d.ple_width, LP = d.layers * d.ple_width;
+    const uint32_t h_tiles = (H + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
     hipStream_t st = s->stream;
+    IrisSession::GemmaCarry& c = s->carry;
     I32GemvArgs ig{};
     {
         const LayerWeights& L = m->layers[l];
         const uint32_t hd = L.head_dim, qw = L.q_rows, kvw = L.kv_rows, qkvw = qw + 2 * kvw;
+        // The layer's input row (its residual) and the free one.
+        int32_t* xin = s->x;
+        int32_t* other = s->attended;
         // 1. q|k|v = W_qkv rms_norm(x, input_layernorm)  (project_tokens :497-579)
         GemvArgs g{};
         g.w = q8_view(L.wqkv);
@@ -602,6 +616,19 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
         g.prologue = PRO_RMSNORM;
         g.norm_w = L.norm_attn;
         g.norm_eps = d.norm_eps;
+        if (carry && c.pending) {
+            // x = (rms_norm(tmp, post_ple) + res) * layer scalar of the layer below
+            g.x = s->tmp;
+            g.prologue = PRO_NORM_RES_NORM;
+            g.ssq_in = s->ssq_x;
+            g.ssq_n = c.slots;
+            g.res_norm_w = c.norm_w;
+            g.res_in = c.res;
+            g.res_scalar = c.scalar;
+            g.res_out = c.spare;
+            xin = c.spare;
+            other = c.res;
+        }
         g.epilogue = EPI_STORE;
         g.out = s->qkv;
         g.out_stride = qkvw;
@@ -654,10 +681,12 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
         g.epilogue = EPI_STORE;
         g.out = s->tmp;
         g.out_stride = H;
+        if (carry) g.ssq_out = s->ssq_x;
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
-        RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_attn, d.norm_eps, s->x, H, 0, s->attended, H, H,
-                                           rows, st));
+        if (!carry)
+            RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_attn, d.norm_eps, s->x, H, 0, s->attended, H, H,
+                                               rows, st));
         // 5. gated = mul(gelu(W_gate f), W_up f), f = rms_norm(attended, pre_ffw)  (:894-913)
         g = GemvArgs{};
         g.w = q8_view(L.wgu);
@@ -667,6 +696,15 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
         g.prologue = PRO_RMSNORM;
         g.norm_w = L.norm_ff;
         g.norm_eps = d.norm_eps;
+        if (carry) {
+            g.x = s->tmp;
+            g.prologue = PRO_NORM_RES_NORM;
+            g.ssq_in = s->ssq_x;
+            g.ssq_n = h_tiles;
+            g.res_norm_w = L.norm_post_attn;
+            g.res_in = xin;
+            g.res_out = other;  // attended
+        }
         g.epilogue = EPI_GEGLU;
         g.out = s->gated;
         g.out_stride = L.ffn;
@@ -681,10 +719,12 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
         g.epilogue = EPI_STORE;
         g.out = s->tmp;
         g.out_stride = H;
+        if (carry) g.ssq_out = s->ssq_x;
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
-        RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ffw, d.norm_eps, s->attended, H, 0, s->attended, H,
-                                           H, rows, st));
+        if (!carry)
+            RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ffw, d.norm_eps, s->attended, H, 0, s->attended,
+                                               H, H, rows, st));
         // 7. PLE block: g = mul(gelu(gate attended), ple); x = rms_norm(proj g) + attended,
         //    times the layer scalar (:931-958)
         ig = I32GemvArgs{};
@@ -697,6 +737,16 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
         ig.out_stride = P;
         ig.aux = s->ple_rows + (size_t)l * P;
         ig.aux_stride = LP;
+        if (carry) {
+            // attended = rms_norm(tmp, post_ffw) + attended, over the layer's input row
+            ig.x = s->tmp;
+            ig.res_in = other;
+            ig.res_norm_w = L.norm_post_ffw;
+            ig.eps = d.norm_eps;
+            ig.ssq_in = s->ssq_x;
+            ig.ssq_n = h_tiles;
+            ig.res_out = xin;
+        }
         RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
         ig = I32GemvArgs{};
         ig.w = L.ple_proj;
@@ -706,17 +756,37 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows) {
         ig.x_stride = P;
         ig.out = s->tmp;
         ig.out_stride = H;
+        if (carry) ig.ssq_out = s->ssq_x;
         RT_CHECK(iris_i32_gemv_launch(ig, rows, st));
-        RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ple, d.norm_eps, s->attended, H, L.layer_scalar,
-                                           s->x, H, H, rows, st));
+        if (carry) {
+            c.pending = true;
+            c.norm_w = L.norm_post_ple;
+            c.scalar = L.layer_scalar;
+            c.res = xin;
+            c.spare = other;
+            c.slots = i32_gemv_slots(H);
+        } else {
+            RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ple, d.norm_eps, s->attended, H, L.layer_scalar,
+                                               s->x, H, H, rows, st));
+        }
     }
     return 0;
 }
 
+// One row with no per-layer checkpoints: the post-norms are carried (the
+// row fits the slot counts and the staged-row limits).
+static bool gemma_carries(const IrisSession* s, uint32_t rows, const CkptSink* sink) {
+    const uint32_t H = s->model->d.hidden;
+    return rows == 1 && !sink && H % 4 == 0 && (H + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS <= GEMV_SSQ_SLOTS &&
+           H <= 4096 && H <= I32_GEMV_MAX_STAGED;
+}
+
 static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
+    const bool carry = gemma_carries(s, rows, sink);
+    s->carry = IrisSession::GemmaCarry{};
     RT_CHECK(gemma_ple(s, rows));
     for (uint32_t l = 0; l < s->model->d.layers; l++) {
-        RT_CHECK(gemma_layer(s, l, rows));
+        RT_CHECK(gemma_layer(s, l, rows, carry));
         RT_CHECK(checkpoint_layer(s, sink, l, rows));
     }
     return 0;
@@ -724,6 +794,7 @@ static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
 
 static int session_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     s->ssq_x_valid = false;
+    s->carry.pending = false;
     if (s->model->d.family == IRIS_FAMILY_GEMMA_DENSE) return gemma_pass(s, rows, sink);
     return mistral_pass(s, rows, sink);
 }
@@ -742,6 +813,17 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     if (rows == 1 && s->ssq_x_valid) {
         g.ssq_in = s->ssq_x;
         g.ssq_n = (d.hidden + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS;
+    }
+    if (rows == 1 && s->carry.pending) {
+        // the last layer's PLE post-norm, carried into the final norm
+        g.x = s->tmp;
+        g.prologue = PRO_NORM_RES_NORM;
+        g.ssq_in = s->ssq_x;
+        g.ssq_n = s->carry.slots;
+        g.res_norm_w = s->carry.norm_w;
+        g.res_in = s->carry.res;
+        g.res_scalar = s->carry.scalar;
+        g.res_out = nullptr;
     }
     g.epilogue = EPI_HEAD_SELECT;
     g.softcap = m->head_softcap;
@@ -1119,7 +1201,7 @@ int iris_session_layer_stage(IrisSession* s, uint32_t layer, const int32_t* in_r
         const size_t P = d.ple_width, LP = (size_t)d.layers * d.ple_width;
         RT_CHECK(hipMemcpy2DAsync(s->ple_rows + (size_t)layer * P, LP * 4, ple_rows, P * 4, P * 4, count,
                                   hipMemcpyHostToDevice, st));
-        RT_CHECK(gemma_layer(s, layer, count));
+        RT_CHECK(gemma_layer(s, layer, count, false));
     } else {
         RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, count, s->rope_sc, st));
         RT_CHECK(mistral_layer(s, layer, count, false, false));

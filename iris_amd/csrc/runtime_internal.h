@@ -78,6 +78,19 @@ struct IrisSession {
     // the residual products and read by the norms that follow them.
     int64_t *ssq_x = nullptr, *ssq_att = nullptr;
     bool ssq_x_valid = false;  // the last pass left ssq_x for the head's norm
+    // gemma-dense one-row passes carry each post-norm into the next product:
+    // the product's row stays in tmp with its sums of squares in ssq_x, to be
+    // rms_norm'ed with norm_w, added to res and scaled by scalar (0 = none).
+    // After the pass, `pending` says the last layer's post-norm is still
+    // carried (for the head).
+    struct GemmaCarry {
+        bool pending = false;
+        const int32_t* norm_w = nullptr;
+        int32_t scalar = 0;
+        int32_t* res = nullptr;    // the residual row
+        int32_t* spare = nullptr;  // the other of x and attended, free
+        uint32_t slots = 0;
+    } carry;
     bool rope_ready = false;   // the last selection left rope_sc for the next one-row pass
     // gemma-dense only: raw q|k|v rows, a product's rows before their norm,
     // the PLE projections and inputs of every layer, the PLE gate output
