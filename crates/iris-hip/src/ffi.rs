@@ -222,5 +222,6 @@ extern "C" {
         score_out: *mut i32,
     ) -> c_int;
     pub fn iris_silu_device(x: *const i32, n: u32, out: *mut i32) -> c_int;
+    pub fn iris_silu_table_device(x: *const i32, n: u32, out: *mut i32) -> c_int;
     pub fn iris_sha256_bytes(data: *const u8, len: u64, out: *mut u8) -> c_int;
 }

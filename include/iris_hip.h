@@ -281,6 +281,12 @@ int iris_attention_numerics(const uint32_t* diff, const uint64_t* e, const uint6
  * it (device pointers; synchronous). No counterpart in the reference. */
 int iris_silu_device(const int32_t* x, uint32_t n, int32_t* out);
 
+/* Numerics check: the same silu through the device's silu table, as the
+ * matrix-core SwiGLU epilogues look it up (device pointers; synchronous; the
+ * table is made on the first call on a device). No counterpart in the
+ * reference. */
+int iris_silu_table_device(const int32_t* x, uint32_t n, int32_t* out);
+
 /* SHA-256 (FIPS 180-4) of `len` bytes into out[32]; the hash
  * iris_session_layer_pass uses. Host code only. */
 int iris_sha256_bytes(const uint8_t* data, uint64_t len, uint8_t* out);

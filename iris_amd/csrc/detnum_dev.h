@@ -394,6 +394,25 @@ __device__ inline int32_t silu(int32_t x) {
     return clamp_i64_to_i32(m_shift_rte(product, 32));
 }
 
+// silu by table. exp_neg_q32(|x| << 16) is zero once the quotient by ln 2
+// reaches 32, i.e. for |x| >= SILU_TAB_HALF; there the divisor is 2^32, the
+// sigmoid 2^32 (or 0 for x < 0) and silu(x) is exactly x (or 0). Inside,
+// silu(x) = tab[x + SILU_TAB_HALF - 1], a table of dn::silu itself.
+constexpr int32_t SILU_TAB_HALF = 1453635;
+constexpr uint32_t SILU_TAB_N = 2u * SILU_TAB_HALF - 1;
+
+// The table index of x (clamped, so the load is always in bounds).
+__device__ __forceinline__ uint32_t silu_tab_index(int32_t x) {
+    const uint32_t u = (uint32_t)x + (uint32_t)(SILU_TAB_HALF - 1);
+    return u < SILU_TAB_N ? u : SILU_TAB_N - 1;
+}
+
+// silu(x) given tab[silu_tab_index(x)].
+__device__ __forceinline__ int32_t silu_from_tab(int32_t x, int32_t looked_up) {
+    const uint32_t u = (uint32_t)x + (uint32_t)(SILU_TAB_HALF - 1);
+    return u < SILU_TAB_N ? looked_up : (x > 0 ? x : 0);
+}
+
 // mistral.rs:84-109 (returns sin, cos in Q30)
 __device__ inline void sin_cos_q30(int64_t angle, int64_t& sin_out, int64_t& cos_out) {
     const int64_t ONE_Q30 = (int64_t)1 << 30;

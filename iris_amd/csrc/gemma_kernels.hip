@@ -113,21 +113,48 @@ __global__ __launch_bounds__(NT) void norm_residual_kernel(const int32_t* a, uin
 // One-row extras (I32GemvArgs): the input formed in LDS as the post-norm
 // and residual of the previous product (norm_residual_kernel's arithmetic),
 // and per-workgroup sums of squares of the outputs.
+constexpr uint32_t I32_ROUND = 8;  // 16-byte loads a lane has in flight per row chunk
+
 __global__ __launch_bounds__(NT) void i32_gemv_kernel(const I32GemvArgs a, uint32_t rows_per_wave) {
     extern __shared__ __align__(16) int32_t s_x[];  // the staged input row (res_in set)
     __shared__ int64_t s_red[NW];
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t t = blockIdx.y;
     const int32_t* xr = a.x + (size_t)t * a.x_stride;
+    const uint32_t c4 = a.cols / 4;
     if (a.res_in) {
+        // Every load of the thread's share first (clamped indices, at most
+        // I32_GEMV_MAX_STAGED / 4 / NT 16-byte loads per array), then the
+        // slots' sum, then the row.
+        constexpr uint32_t PER = I32_GEMV_MAX_STAGED / 4 / NT;
+        int4 xv[PER], wv[PER], rv[PER];
+#pragma unroll
+        for (uint32_t u = 0; u < PER; u++) xv[u] = ((const int4*)xr)[min(u * NT + tid, c4 - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < PER; u++) wv[u] = ((const int4*)a.res_norm_w)[min(u * NT + tid, c4 - 1)];
+#pragma unroll
+        for (uint32_t u = 0; u < PER; u++) rv[u] = ((const int4*)a.res_in)[min(u * NT + tid, c4 - 1)];
+        int64_t sl[I32_GEMV_MAX_SLOTS / 64];
+#pragma unroll
+        for (uint32_t u = 0; u < I32_GEMV_MAX_SLOTS / 64; u++) sl[u] = a.ssq_in[min(lane + 64 * u, a.ssq_n - 1)];
         int64_t ss = 0;
-        for (uint32_t i = lane; i < a.ssq_n; i += 64) ss = dn::acc_add_sat(ss, a.ssq_in[i]);
+#pragma unroll
+        for (uint32_t u = 0; u < I32_GEMV_MAX_SLOTS / 64; u++)
+            if (lane + 64 * u < a.ssq_n) ss = dn::acc_add_sat(ss, sl[u]);
         const int32_t scale = dn::rms_scale_from_sum(wave_sum_sat(ss), a.cols, a.eps);
         const bool store = a.res_out != nullptr && blockIdx.x == 0;
-        for (uint32_t i = tid; i < a.cols; i += NT) {
-            const int32_t y = dn::add_sat(dn::mul_sat(dn::mul_sat(xr[i], scale), a.res_norm_w[i]), a.res_in[i]);
-            s_x[i] = y;
-            if (store) a.res_out[i] = y;
+#pragma unroll
+        for (uint32_t u = 0; u < PER; u++) {
+            const uint32_t i = u * NT + tid;
+            if (i < c4) {
+                int4 y;
+                y.x = dn::add_sat(dn::mul_sat(dn::mul_sat(xv[u].x, scale), wv[u].x), rv[u].x);
+                y.y = dn::add_sat(dn::mul_sat(dn::mul_sat(xv[u].y, scale), wv[u].y), rv[u].y);
+                y.z = dn::add_sat(dn::mul_sat(dn::mul_sat(xv[u].z, scale), wv[u].z), rv[u].z);
+                y.w = dn::add_sat(dn::mul_sat(dn::mul_sat(xv[u].w, scale), wv[u].w), rv[u].w);
+                ((int4*)s_x)[i] = y;
+                if (store) ((int4*)a.res_out)[i] = y;
+            }
         }
         __syncthreads();
         xr = s_x;
@@ -137,15 +164,25 @@ __global__ __launch_bounds__(NT) void i32_gemv_kernel(const I32GemvArgs a, uint3
     for (uint32_t j = 0; j < rows_per_wave; j++) {
         const uint32_t row = base + j * NW + wave;
         if (row >= a.rows) break;
-        const int32_t* wr = a.w + (size_t)row * a.cols;
+        const int4* wr = (const int4*)(a.w + (size_t)row * a.cols);
         uint64_t acc = 0;
-        for (uint32_t k = lane * 4; k < a.cols; k += 256) {
-            const int4 xv = *(const int4*)(xr + k);
-            const int4 wv = *(const int4*)(wr + k);
-            acc += (uint64_t)((int64_t)xv.x * wv.x);
-            acc += (uint64_t)((int64_t)xv.y * wv.y);
-            acc += (uint64_t)((int64_t)xv.z * wv.z);
-            acc += (uint64_t)((int64_t)xv.w * wv.w);
+        // I32_ROUND loads of the row in flight at once (clamped, dropped
+        // past the row's end).
+        for (uint32_t k0 = 0; k0 < c4; k0 += 64 * I32_ROUND) {
+            int4 wv[I32_ROUND], xv[I32_ROUND];
+#pragma unroll
+            for (uint32_t u = 0; u < I32_ROUND; u++) wv[u] = wr[min(k0 + u * 64 + lane, c4 - 1)];
+#pragma unroll
+            for (uint32_t u = 0; u < I32_ROUND; u++) xv[u] = ((const int4*)xr)[min(k0 + u * 64 + lane, c4 - 1)];
+#pragma unroll
+            for (uint32_t u = 0; u < I32_ROUND; u++) {
+                if (k0 + u * 64 + lane < c4) {
+                    acc += (uint64_t)((int64_t)xv[u].x * wv[u].x);
+                    acc += (uint64_t)((int64_t)xv[u].y * wv[u].y);
+                    acc += (uint64_t)((int64_t)xv[u].z * wv[u].z);
+                    acc += (uint64_t)((int64_t)xv[u].w * wv[u].w);
+                }
+            }
         }
         for (int off = 32; off >= 1; off >>= 1) acc += __shfl_xor(acc, off);
         int32_t v = dn::requantize((int64_t)acc);
@@ -235,11 +272,15 @@ uint32_t i32_gemv_slots(uint32_t rows) {
 
 int iris_i32_gemv_launch(const I32GemvArgs& a, uint32_t tokens, hipStream_t stream) {
     if (a.rows == 0 || a.cols == 0 || a.cols % 4 || a.x_stride % 4) return IRIS_E_INVALID;
+    if (((uintptr_t)a.x | (uintptr_t)a.w) & 15) return IRIS_E_INVALID;
     if (tokens == 0) return 0;
     if ((a.res_in || a.ssq_out) && tokens != 1) return IRIS_E_INVALID;
     size_t shmem = 0;
     if (a.res_in) {
-        if (!a.res_norm_w || !a.ssq_in || a.ssq_n == 0 || a.cols > I32_GEMV_MAX_STAGED) return IRIS_E_INVALID;
+        if (!a.res_norm_w || !a.ssq_in || a.ssq_n == 0 || a.ssq_n > I32_GEMV_MAX_SLOTS || a.cols > I32_GEMV_MAX_STAGED)
+            return IRIS_E_INVALID;
+        if (((uintptr_t)a.x | (uintptr_t)a.res_in | (uintptr_t)a.res_norm_w | (uintptr_t)a.res_out) & 15)
+            return IRIS_E_INVALID;
         if (a.res_out && (a.res_out == a.res_in || a.res_out == a.x)) return IRIS_E_INVALID;
         shmem = (size_t)a.cols * 4;
     }

@@ -3,7 +3,12 @@
 
 #include "q8_internal.h"
 
-constexpr uint32_t ATTN_MAX_KEYS = 4096;      // visible keys one query attends to
+// Visible keys one query attends to: the matrix-core prefill's value sums
+// stay in int32 below 2^16 keys (each 64-key step adds at most 2 * 64 * 2^14).
+constexpr uint32_t ATTN_MAX_KEYS = 65535;
+// Keys whose weights one workgroup holds in LDS at a time; longer views take
+// the tiled paths (scores re-read or re-formed per pass).
+constexpr uint32_t ATTN_TILE_KEYS = 4096;
 constexpr uint32_t ATTN_MAX_HEAD_DIM = 256;
 
 // Work space of the multi-row attention: the signed byte digits (four
@@ -139,6 +144,9 @@ int iris_norm_residual_launch(const int32_t* a, uint32_t a_stride, const int32_t
                               uint32_t res_stride, int32_t scalar, int32_t* out, uint32_t out_stride, uint32_t n,
                               uint32_t rows, hipStream_t stream);
 int iris_i32_gemv_launch(const I32GemvArgs& a, uint32_t tokens, hipStream_t stream);
+// The device's silu table (dn::SILU_TAB_N values of dn::silu), made on the
+// first call on a device and kept until the process ends.
+int iris_silu_table(const int32_t** out);
 int iris_ple_prepare_launch(const PleArgs& a, uint32_t segments, uint32_t rows, hipStream_t stream);
 // (sin, cos) in Q30 (mistral.rs:84-109) of position * inv_freq[j] for the
 // `rows` positions from *d_pos and j < half: out[row][j][2].

@@ -1,5 +1,8 @@
 // The non-product kernels of the token loop: exact attention over the
 // device KV cache and the prompt embedding gather.
+#include <map>
+#include <mutex>
+
 #include "attn_common.h"
 #include "detnum_dev.h"
 #include "layer_kernels.h"
@@ -28,66 +31,175 @@ __global__ __launch_bounds__(ATTN_MAX_THREADS) void attention_kernel(const AttnA
 // transposed cache (consecutive lanes read consecutive positions of one
 // dimension); the groups' partial sums meet by shuffles, then across the
 // four waves in LDS.
+// Workgroup (head, y) takes the 64-position chunks y, y + gridDim.y, ...
+// of the view (one chunk each for views up to 64 * gridDim.y keys).
 template <uint32_t HD>
 __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
     constexpr uint32_t DPG = HD / 16;
     __shared__ int32_t s_q[HD];
     __shared__ uint64_t s_part[4][64];
-    const uint32_t head = blockIdx.x, c0 = blockIdx.y * 64, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t head = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
-    if (c0 > pos || c0 + 63 < start) return;  // the chunk holds no visible key
+    // The first chunk of this workgroup that holds a visible key (every
+    // later one up to the position does too).
+    uint32_t c = blockIdx.y;
+    if (c * 64 + 63 < start) {
+        const uint32_t behind = start - (c * 64 + 63), step = 64 * gridDim.y;
+        c += (behind + step - 1) / step * gridDim.y;
+    }
+    if (c * 64 > pos) return;
     const uint32_t kvh = head / (a.heads / a.kv_heads);
     // The query element this thread stages, loaded first (waiting for it
     // does not wait for the key loads issued after it).
     const int32_t qv = a.q[(size_t)head * HD + tid % HD];
     const uint32_t kq = lane & 15, grp = wave * 4 + (lane >> 4);
-    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + grp * DPG) * a.k_pos_stride + c0 + 4 * kq;
+    const int32_t* kb = a.k_cache + ((size_t)kvh * HD + grp * DPG) * a.k_pos_stride + 4 * kq;
     int4 kv[DPG];
+    auto load_keys = [&](uint32_t chunk) {
 #pragma unroll
-    for (uint32_t i = 0; i < DPG; i++) kv[i] = *(const int4*)(kb + (size_t)i * a.k_pos_stride);
+        for (uint32_t i = 0; i < DPG; i++) kv[i] = *(const int4*)(kb + (size_t)i * a.k_pos_stride + chunk * 64);
+    };
+    load_keys(c);
     if (tid < HD) s_q[tid] = qv;
     lds_barrier();
-    uint64_t dot[4] = {0, 0, 0, 0};
+    for (;;) {
+        uint64_t dot[4] = {0, 0, 0, 0};
 #pragma unroll
-    for (uint32_t i = 0; i < DPG; i++) {
-        const int64_t q = s_q[grp * DPG + i];
-        dot[0] += (uint64_t)(q * kv[i].x);
-        dot[1] += (uint64_t)(q * kv[i].y);
-        dot[2] += (uint64_t)(q * kv[i].z);
-        dot[3] += (uint64_t)(q * kv[i].w);
+        for (uint32_t i = 0; i < DPG; i++) {
+            const int64_t q = s_q[grp * DPG + i];
+            dot[0] += (uint64_t)(q * kv[i].x);
+            dot[1] += (uint64_t)(q * kv[i].y);
+            dot[2] += (uint64_t)(q * kv[i].z);
+            dot[3] += (uint64_t)(q * kv[i].w);
+        }
+        const uint32_t c0 = c * 64;
+        c += gridDim.y;
+        const bool more = c * 64 <= pos;
+        if (more) load_keys(c);
+#pragma unroll
+        for (uint32_t off = 16; off < 64; off <<= 1)
+#pragma unroll
+            for (int k = 0; k < 4; k++) dot[k] += __shfl_xor(dot[k], off);
+        if (lane < 16)
+#pragma unroll
+            for (int k = 0; k < 4; k++) s_part[wave][4 * kq + k] = dot[k];
+        lds_barrier();
+        if (tid < 64) {
+            const uint64_t sum = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
+            const int32_t sc =
+                a.scaled ? dn::scaled_score_from_sum((int64_t)sum, a.scale_q32) : dn::requantize((int64_t)sum);
+            a.scores[(size_t)head * a.k_pos_stride + c0 + tid] = sc;  // positions outside the view are never read
+        }
+        if (!more) break;
+        lds_barrier();  // s_part is read before the next chunk overwrites it
     }
+}
+
+constexpr uint32_t VAL_NT = 512, VAL_NW = VAL_NT / 64;
+constexpr uint32_t VAL_DS = 32;  // dimensions per values workgroup
+
+struct ValuesSmem {
+    int32_t w[ATTN_TILE_KEYS];  // weights
+    int64_t part[64 * VAL_DS];
+    ArgMax am[VAL_NW];
+    uint64_t sum[VAL_NW];
+    int32_t wsum[VAL_NW];
+};
+
+// The values workgroup for a view longer than ATTN_TILE_KEYS: the first
+// maximum and the exp sum from the stored scores (two reads), then tile by
+// tile the weights (exp terms formed again) and their weighted values. The
+// first maximum's residual is added at the end as resid * v: the weighted
+// sum is linear and wraps, so this equals the reference's adjusted weight.
+template <uint32_t HD>
+__device__ void values_long(const AttnArgs& a, ValuesSmem& sm, uint32_t head, uint32_t slice, uint32_t kvh,
+                            uint32_t start, uint32_t n) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int32_t* sb = a.scores + (size_t)head * a.k_pos_stride + start;
+    uint64_t best = 0;
+    for (uint32_t j = tid; j < n; j += VAL_NT) {
+        const uint64_t k = ((uint64_t)((uint32_t)sb[j] ^ 0x80000000u) << 32) | (uint32_t)~j;
+        best = k > best ? k : best;
+    }
+    best = wave_max_u64(best);
+    if (lane == 0) sm.am[wave] = ArgMax{(int32_t)((uint32_t)(best >> 32) ^ 0x80000000u), ~(uint32_t)best};
+    __syncthreads();
+    ArgMax m = sm.am[0];
+    for (uint32_t i = 1; i < VAL_NW; i++) m = argmax_combine(m, sm.am[i]);
+    auto exp_term = [&](uint32_t j) -> uint64_t {
+        const int64_t diff = (int64_t)m.v - sb[j];
+        return diff < (1 << 20) ? dn::softmax_exp_diff((uint32_t)diff) : 0;
+    };
+    // Terms of at most 2^32 each: no saturation below 2^31 keys.
+    uint64_t part = 0;
+    for (uint32_t j = tid; j < n; j += VAL_NT) part += exp_term(j);
+    part = wave_sum_u64(part);
+    if (lane == 0) sm.sum[wave] = part;
+    __syncthreads();
+    uint64_t total = 0;
+    for (uint32_t i = 0; i < VAL_NW; i++) total += sm.sum[i];
+    const double w_scale = 65536.0 / (double)total, q_scale = 4294967296.0 / (double)total;
+    const uint32_t kr = tid / 8, d4 = (tid % 8) * 4;
+    const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * HD + slice * VAL_DS + d4;
+    // The weights sum to 2^16 plus at most one half per key: a plain sum.
+    int32_t wpart = 0;
+    uint64_t acc[4] = {0, 0, 0, 0};
+    for (uint32_t t0 = 0; t0 < n; t0 += ATTN_TILE_KEYS) {
+        const uint32_t tn = min(ATTN_TILE_KEYS, n - t0);
+        for (uint32_t j = tid; j < tn; j += VAL_NT) {
+            const int32_t w = dn::softmax_weight_fast(exp_term(t0 + j), total, w_scale, q_scale);
+            sm.w[j] = w;
+            wpart += w;
+        }
+        __syncthreads();
+        for (uint32_t key = kr; key < tn; key += 64) {
+            const int4 v = *(const int4*)(vb + (size_t)(t0 + key) * a.kv_stride);
+            const int64_t w = sm.w[key];
+            acc[0] += (uint64_t)(w * v.x);
+            acc[1] += (uint64_t)(w * v.y);
+            acc[2] += (uint64_t)(w * v.z);
+            acc[3] += (uint64_t)(w * v.w);
+        }
+        __syncthreads();
+    }
+    wpart = (int32_t)wave_sum_u64((uint64_t)(uint32_t)wpart);
+    if (lane == 0) sm.wsum[wave] = wpart;
 #pragma unroll
-    for (uint32_t off = 16; off < 64; off <<= 1)
-#pragma unroll
-        for (int c = 0; c < 4; c++) dot[c] += __shfl_xor(dot[c], off);
-    if (lane < 16)
-#pragma unroll
-        for (int c = 0; c < 4; c++) s_part[wave][4 * kq + c] = dot[c];
-    lds_barrier();
-    if (tid < 64) {
-        const uint64_t sum = s_part[0][tid] + s_part[1][tid] + s_part[2][tid] + s_part[3][tid];
-        const int32_t sc = a.scaled ? dn::scaled_score_from_sum((int64_t)sum, a.scale_q32) : dn::requantize((int64_t)sum);
-        a.scores[(size_t)head * a.k_pos_stride + c0 + tid] = sc;  // positions outside the view are never read
+    for (int c = 0; c < 4; c++) sm.part[kr * VAL_DS + d4 + c] = (int64_t)acc[c];
+    __syncthreads();
+    if (tid < VAL_DS) {
+        int32_t wsum = 0;
+        for (uint32_t i = 0; i < VAL_NW; i++) wsum = dn::add_sat(wsum, sm.wsum[i]);
+        uint64_t t = 0;
+        for (uint32_t r = 0; r < 64; r++) t += (uint64_t)sm.part[r * VAL_DS + tid];
+        const int64_t resid = dn::sub_sat(dn::ONE_ACT, wsum);
+        t += (uint64_t)(resid * a.v_cache[(size_t)(start + m.i) * a.kv_stride + (size_t)kvh * HD + slice * VAL_DS + tid]);
+        a.ctx[(size_t)head * HD + slice * VAL_DS + tid] = dn::requantize((int64_t)t);
     }
 }
 
 template <uint32_t HD>
 __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
-    constexpr uint32_t NT = 512, NWV = NT / 64;
-    constexpr uint32_t DS = 32;                             // dimensions per workgroup
+    constexpr uint32_t NT = VAL_NT, NWV = VAL_NW;
+    constexpr uint32_t DS = VAL_DS;                         // dimensions per workgroup
     constexpr uint32_t VR = 16;                             // 64-key value rounds loaded before the softmax
-    constexpr uint32_t EPT = ATTN_MAX_KEYS / NT;            // keys per thread, at most
-    __shared__ int32_t s_w[ATTN_MAX_KEYS];                  // weights
-    __shared__ int64_t s_part[64 * DS];
-    __shared__ ArgMax s_am[NWV];
-    __shared__ uint64_t s_sum[NWV];
-    __shared__ int32_t s_wsum[NWV];
+    constexpr uint32_t EPT = ATTN_TILE_KEYS / NT;           // keys per thread, at most
+    __shared__ ValuesSmem sm;
+    int32_t* s_w = sm.w;
+    int64_t* s_part = sm.part;
+    ArgMax* s_am = sm.am;
+    uint64_t* s_sum = sm.sum;
+    int32_t* s_wsum = sm.wsum;
     const uint32_t head = blockIdx.x, slice = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = head / (a.heads / a.kv_heads);
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
     const uint32_t n = pos - start + 1;
+    if (n > ATTN_TILE_KEYS) {  // uniform over the launch
+        values_long<HD>(a, sm, head, slice, kvh, start, n);
+        return;
+    }
 
     // 1. This thread's scores (keys tid + NT*u, increasing), then the slice's
     // value rows; both loads are unconditional (clamped indices), the scores
@@ -125,7 +237,7 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
     for (uint32_t i = 1; i < NWV; i++) m = argmax_combine(m, s_am[i]);
 
     // 3. Exp terms (non-negative: their sum is order-free and cannot
-    // saturate for 4096 keys) and 4. the weights and their sum.
+    // saturate for ATTN_TILE_KEYS keys) and 4. the weights and their sum.
     uint64_t ev[EPT];
     uint64_t part = 0;
 #pragma unroll
@@ -152,8 +264,8 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
             wpart += w;
         }
     }
-    // Weights are non-negative and at most 4096 * 2^16 in all: the
-    // saturating sum never saturates, a plain sum is the same.
+    // Weights are non-negative and sum to 2^16 plus at most one half per
+    // key: the saturating sum never saturates, a plain sum is the same.
     wpart = (int32_t)wave_sum_u64((uint64_t)(uint32_t)wpart);
     if (lane == 0) s_wsum[wave] = wpart;
     lds_barrier();
@@ -197,7 +309,9 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
 
 template <uint32_t HD>
 int attention_decode_launch(const AttnArgs& a, hipStream_t stream) {
-    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(a.heads, a.k_pos_stride / 64), dim3(256), 0, stream, a);
+    // Up to 32 chunk workgroups per head (longer views loop over chunks).
+    const uint32_t chunks = min(a.k_pos_stride / 64, 32u);
+    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(a.heads, chunks), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(attn_values_kernel<HD>, dim3(a.heads, HD / 32), dim3(512), 0, stream, a);
     return (int)hipGetLastError();
 }
@@ -239,6 +353,17 @@ __global__ __launch_bounds__(256) void silu_kernel(const int32_t* x, uint32_t n,
     if (i < n) out[i] = dn::silu(x[i]);
 }
 
+__global__ __launch_bounds__(256) void silu_table_kernel(int32_t* tab) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < dn::SILU_TAB_N) tab[i] = dn::silu((int32_t)i - (dn::SILU_TAB_HALF - 1));
+}
+
+__global__ __launch_bounds__(256) void silu_lookup_kernel(const int32_t* tab, const int32_t* x, uint32_t n,
+                                                          int32_t* out) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) out[i] = dn::silu_from_tab(x[i], tab[dn::silu_tab_index(x[i])]);
+}
+
 // The pass position and the selection step of a session, set on its stream.
 __global__ void set_counters_kernel(int32_t* d_pos, int32_t pos, int32_t* d_step, int32_t step) {
     if (threadIdx.x == 0) {
@@ -258,6 +383,47 @@ extern "C" int iris_silu_device(const int32_t* d_x, uint32_t n, int32_t* d_out) 
     if (n == 0) return 0;
     if (!d_x || !d_out) return IRIS_E_INVALID;
     hipLaunchKernelGGL(silu_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, d_x, n, d_out);
+    hipError_t st = hipGetLastError();
+    if (st == hipSuccess) st = hipDeviceSynchronize();
+    return (int)st;
+}
+
+int iris_silu_table(const int32_t** out) {
+    // One table per device, made on first use and kept until the process ends.
+    static std::mutex mu;
+    static std::map<int, int32_t*> tables;
+    *out = nullptr;
+    int dev = 0;
+    hipError_t st = hipGetDevice(&dev);
+    if (st != hipSuccess) return (int)st;
+    std::lock_guard<std::mutex> lock(mu);
+    auto it = tables.find(dev);
+    if (it != tables.end()) {
+        *out = it->second;
+        return 0;
+    }
+    int32_t* tab = nullptr;
+    st = hipMalloc((void**)&tab, (size_t)dn::SILU_TAB_N * 4);
+    if (st != hipSuccess) return IRIS_E_NOMEM;
+    hipLaunchKernelGGL(silu_table_kernel, dim3((dn::SILU_TAB_N + 255) / 256), dim3(256), 0, nullptr, tab);
+    st = hipGetLastError();
+    if (st == hipSuccess) st = hipDeviceSynchronize();
+    if (st != hipSuccess) {
+        hipFree(tab);
+        return (int)st;
+    }
+    tables[dev] = tab;
+    *out = tab;
+    return 0;
+}
+
+extern "C" int iris_silu_table_device(const int32_t* d_x, uint32_t n, int32_t* d_out) {
+    if (n == 0) return 0;
+    if (!d_x || !d_out) return IRIS_E_INVALID;
+    const int32_t* tab = nullptr;
+    int rc = iris_silu_table(&tab);
+    if (rc) return rc;
+    hipLaunchKernelGGL(silu_lookup_kernel, dim3((n + 255) / 256), dim3(256), 0, nullptr, tab, d_x, n, d_out);
     hipError_t st = hipGetLastError();
     if (st == hipSuccess) st = hipDeviceSynchronize();
     return (int)st;

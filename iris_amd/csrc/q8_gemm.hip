@@ -249,6 +249,7 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
     const uint32_t wr = wave % (G::WAVES / 2), wt = wave / (G::WAVES / 2);
     const Q8View& w = a.w;
     const bool pairs = a.epilogue == EPI_SWIGLU || a.epilogue == EPI_GEGLU;
+    const bool table = a.epilogue == EPI_SWIGLU && a.silu_tab != nullptr;
     int32_t* sC = (int32_t*)smem;
 #pragma unroll
     for (int i = 0; i < G::RI; i++) {
@@ -257,7 +258,7 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
             const uint32_t tl = (wt * TTW + j) * 32 + (lane & 31);
             int32_t v[16];
             block_values(i, j, v);
-            if (pairs) {
+            if (pairs && !table) {
                 // Rows e and e + 1 (e even) are a gate/up pair in this lane:
                 // the activation runs here, once per pair, every lane busy.
 #pragma unroll
@@ -274,7 +275,33 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
         }
     }
     __syncthreads();
-    if (pairs) {
+    if (table) {
+        // out[token][row / 2] = mul_sat(silu(gate), up) from the parked
+        // [row][token] block, TB pairs per thread at a time: their table
+        // loads (tab[gate], exact: dn::silu of every input that needs it)
+        // are in flight together.
+        constexpr uint32_t PAIRS = ROWS / 2 * NTOK, TB = 8;
+        static_assert(PAIRS % (G::THREADS * TB) == 0, "whole batches");
+        for (uint32_t c0 = tid; c0 < PAIRS; c0 += G::THREADS * TB) {
+            int32_t gate[TB], up[TB], looked[TB];
+#pragma unroll
+            for (uint32_t u = 0; u < TB; u++) {
+                const uint32_t c = c0 + u * G::THREADS, pl = c % (ROWS / 2), tl = c / (ROWS / 2);
+                gate[u] = sC[2 * pl * STRIDE + tl];
+                up[u] = sC[(2 * pl + 1) * STRIDE + tl];
+            }
+#pragma unroll
+            for (uint32_t u = 0; u < TB; u++) looked[u] = a.silu_tab[dn::silu_tab_index(gate[u])];
+#pragma unroll
+            for (uint32_t u = 0; u < TB; u++) {
+                const uint32_t c = c0 + u * G::THREADS, pl = c % (ROWS / 2), tl = c / (ROWS / 2);
+                const uint32_t pair = rt0 * 16 + pl, token = tt0 * 32 + tl;
+                if (2 * pair < w.rows && token < a.tokens)
+                    a.out[(size_t)token * a.out_stride + pair] =
+                        dn::mul_sat(dn::silu_from_tab(gate[u], looked[u]), up[u]);
+            }
+        }
+    } else if (pairs) {
         // out[token][row / 2] for the block's ROWS / 2 pairs.
         for (uint32_t c = tid; c < ROWS / 2 * NTOK; c += G::THREADS) {
             const uint32_t pl = c % (ROWS / 2), tl = c / (ROWS / 2);

@@ -120,6 +120,9 @@ struct GemvArgs {
     const int32_t* residual;
     uint32_t residual_stride;
     int32_t softcap;
+    // EPI_SWIGLU of the matrix-core products: the device's silu table
+    // (iris_silu_table); null computes each silu.
+    const int32_t* silu_tab;
     // EPI_ROPE_KV
     const int32_t* d_pos;       // absolute position of token 0 of this launch
     const int64_t* inv_freq;    // head_dim/2 Q32.32 angles per position
@@ -146,8 +149,9 @@ struct GemvArgs {
     // GEMM when this work space is given (null: the GEMV path).
     int8_t* planes;             // gemm_planes_bytes(cols, tokens): 5 digit planes, MFMA-operand tiled
     int32_t* token_limbs;       // [2][tokens]: digits each token's activations need, then its rms_norm scale
-    // One-token launches only. ssq_out (EPI_RESIDUAL): each tile's saturating
-    // sum of the squares of its outputs, slot [tile]. ssq_in (PRO_RMSNORM):
+    // One-token launches only. ssq_out (EPI_RESIDUAL or EPI_STORE): each
+    // tile's saturating sum of the squares of its outputs, slot [tile].
+    // ssq_in (PRO_RMSNORM, PRO_NORM_RES_NORM: the first norm):
     // such slots of the row being normed, ssq_n of them (at most
     // GEMV_SSQ_SLOTS): the norm's sum of squares is their saturating sum
     // (non-negative terms: the same in any grouping), so the workgroups skip

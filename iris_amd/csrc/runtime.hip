@@ -500,6 +500,7 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
         g.norm_w = L.norm_ff;
         g.norm_eps = d.norm_eps;
         g.epilogue = EPI_SWIGLU;
+        g.silu_tab = s->silu_tab;
         g.out = s->gated;
         g.out_stride = d.ffn;
         if (slots) {
@@ -983,6 +984,8 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
         for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++)
             for (Q8GpuMatrix* w : {m->layers[l].wqkv, m->layers[l].wo, m->layers[l].wgu, m->layers[l].wdown})
                 if (st == hipSuccess) st = (hipError_t)iris_q8_prepare_fold(w, s->stream);
+        // The matrix-core SwiGLU epilogues look silu up.
+        if (d.family != IRIS_FAMILY_GEMMA_DENSE && st == hipSuccess) st = (hipError_t)iris_silu_table(&s->silu_tab);
         size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
         if (st == hipSuccess) st = hipMalloc((void**)&s->planes, gemm_planes_bytes((uint32_t)widest, max_rows));
         alloc(&s->token_limbs, 2 * (size_t)max_rows);

@@ -97,6 +97,7 @@ struct IrisSession {
     int32_t *qkv = nullptr, *tmp = nullptr, *ple_proj = nullptr, *ple_rows = nullptr, *ple_gated = nullptr;
     // digit planes of a multi-row pass's activations for the MFMA products
     int8_t* planes = nullptr;        // gemm_planes_bytes(widest product input, max_rows)
+    const int32_t* silu_tab = nullptr;  // mistral-dense: the device's silu table (not owned)
     int32_t* token_limbs = nullptr;  // [2][max_rows]: digit counts, norm scales
     int32_t *logits = nullptr, *ids = nullptr, *tokens = nullptr;
     int32_t *d_pos = nullptr, *d_step = nullptr;

@@ -159,18 +159,23 @@ def test_long_context_decode_matches_oracle(family):
 @pytest.mark.timeout(600)
 def test_silu_every_input():
     # All 2^32 Q16.16 inputs, in chunks of 2^25: the device silu (the SwiGLU
-    # gate of the product epilogues) against the oracle's silu (mistral.rs:59-77).
+    # gate of the product epilogues) and the table lookup of the matrix-core
+    # epilogues (the table inside |x| < 1453635, x or 0 outside) against the
+    # oracle's silu (mistral.rs:59-77).
     chunk = 1 << 25
     dx = native.DeviceBuffer(4 * chunk)
     dout = native.DeviceBuffer(4 * chunk)
-    bad = 0
+    bad = bad_table = 0
     for c in range((1 << 32) // chunk):
         x = (np.arange(chunk, dtype=np.int64) + (c * chunk - (1 << 31))).astype(np.int32)
         native.check(native.lib().iris_memcpy_h2d(dx.ptr, x.ctypes.data, x.nbytes), "copy")
         native.check(native.lib().iris_silu_device(dx.ptr, chunk, dout.ptr), "silu")
         got = dout.to_array(np.int32, (chunk,))
+        native.check(native.lib().iris_silu_table_device(dx.ptr, chunk, dout.ptr), "silu table")
+        got_table = dout.to_array(np.int32, (chunk,))
         want = cpu.silu_many(x)
         bad += int(np.count_nonzero(got != want))
+        bad_table += int(np.count_nonzero(got_table != want))
         if c % 32 == 31:
-            print(f"silu: {(c + 1) * chunk} inputs checked, {bad} differ", flush=True)
-    assert bad == 0
+            print(f"silu: {(c + 1) * chunk} inputs checked, {bad} differ, {bad_table} by table", flush=True)
+    assert bad == 0 and bad_table == 0
