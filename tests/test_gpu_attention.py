@@ -83,9 +83,14 @@ def _check_pass(m, rows, max_positions=None):
     dm.free()
 
 
-@pytest.mark.parametrize("head_dim,heads,kv_heads,rows", [(128, 8, 2, 150), (64, 16, 2, 77), (128, 4, 1, 17)])
+@pytest.mark.parametrize("head_dim,heads,kv_heads,rows", [
+    (128, 8, 2, 150), (64, 16, 2, 77), (128, 4, 1, 17),
+    (64, 4, 2, 70), (128, 8, 8, 40), (256, 8, 1, 1030), (256, 16, 2, 520), (256, 8, 1, 90)])
 def test_prefill_attention_mistral(head_dim, heads, kv_heads, rows):
-    # GQA groups of four and eight, 1..3 key steps, partial query tiles.
+    # GQA groups of one, two, four and eight (a workgroup's four heads on one
+    # to four KV heads), head sizes 64, 128 and 256 (four value passes, from
+    # 128 workgroups on: 1030 and 520 rows; 90 rows take the one-row
+    # routine), partial query tiles and key steps.
     m = synth.mistral_model(512, 2, heads, kv_heads, head_dim, 512, 512, seed=31 + head_dim + rows)
     _check_pass(m, rows, max_positions=rows + 40)
 
