@@ -1,6 +1,7 @@
 // The non-product kernels of the token loop: exact attention over the
 // device KV cache and the prompt embedding gather.
 #include <map>
+#include <numeric>
 #include <mutex>
 
 #include "attn_common.h"
@@ -31,22 +32,44 @@ __global__ __launch_bounds__(ATTN_MAX_THREADS) void attention_kernel(const AttnA
 // transposed cache (consecutive lanes read consecutive positions of one
 // dimension); the groups' partial sums meet by shuffles, then across the
 // four waves in LDS.
-// Workgroup (head, y) takes the 64-position chunks y, y + gridDim.y, ...
-// of the view (one chunk each for views up to 64 * gridDim.y keys).
+// The decode kernels' workgroups in XCD order. A data unit is one KV head's
+// chunk (scores) or dimension slice (values), read by the `group` query
+// heads that share the KV head; workgroup L runs on XCD L % 8 (workgroups are
+// dealt to the eight XCDs in turn). When the units fill the XCDs evenly,
+// each unit's workgroups go to one XCD, so its keys or values come from
+// memory once into that XCD's L2 rather than once per query head. Returns
+// (query head, chunk or slice) of workgroup L of heads * per_head.
+__device__ __forceinline__ uint2 xcd_head_order(const AttnArgs& a, uint32_t L, uint32_t per_head) {
+    const uint32_t group = a.heads / a.kv_heads, units = a.kv_heads * per_head;
+    uint32_t u, r;
+    if (units % 8 == 0) {
+        const uint32_t q = L / 8;
+        u = L % 8 + 8 * (q / group);
+        r = q % group;
+    } else {
+        u = L / group;
+        r = L % group;
+    }
+    return make_uint2((u % a.kv_heads) * group + r, u / a.kv_heads);
+}
+
+// Workgroup (head, y) takes the 64-position chunks y, y + chunks, ... of
+// the view (one chunk each for views up to 64 * chunks keys).
 template <uint32_t HD>
-__global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint32_t chunks) {
     constexpr uint32_t DPG = HD / 16;
     __shared__ int32_t s_q[HD];
     __shared__ uint64_t s_part[4][64];
-    const uint32_t head = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint2 hy = xcd_head_order(a, blockIdx.x, chunks);
+    const uint32_t head = hy.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
     // The first chunk of this workgroup that holds a visible key (every
     // later one up to the position does too).
-    uint32_t c = blockIdx.y;
+    uint32_t c = hy.y;
     if (c * 64 + 63 < start) {
-        const uint32_t behind = start - (c * 64 + 63), step = 64 * gridDim.y;
-        c += (behind + step - 1) / step * gridDim.y;
+        const uint32_t behind = start - (c * 64 + 63), step = 64 * chunks;
+        c += (behind + step - 1) / step * chunks;
     }
     if (c * 64 > pos) return;
     const uint32_t kvh = head / (a.heads / a.kv_heads);
@@ -74,7 +97,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a) {
             dot[3] += (uint64_t)(q * kv[i].w);
         }
         const uint32_t c0 = c * 64;
-        c += gridDim.y;
+        c += chunks;
         const bool more = c * 64 <= pos;
         if (more) load_keys(c);
 #pragma unroll
@@ -191,7 +214,8 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
     ArgMax* s_am = sm.am;
     uint64_t* s_sum = sm.sum;
     int32_t* s_wsum = sm.wsum;
-    const uint32_t head = blockIdx.x, slice = blockIdx.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint2 hs = xcd_head_order(a, blockIdx.x, HD / VAL_DS);
+    const uint32_t head = hs.x, slice = hs.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = head / (a.heads / a.kv_heads);
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
@@ -309,10 +333,13 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
 
 template <uint32_t HD>
 int attention_decode_launch(const AttnArgs& a, hipStream_t stream) {
-    // Up to 32 chunk workgroups per head (longer views loop over chunks).
-    const uint32_t chunks = min(a.k_pos_stride / 64, 32u);
-    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(a.heads, chunks), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(attn_values_kernel<HD>, dim3(a.heads, HD / 32), dim3(512), 0, stream, a);
+    // Up to 32 chunk workgroups per head (longer views loop over chunks),
+    // rounded up so that the KV heads' chunks fill the XCDs evenly (the
+    // extra workgroups find no visible key).
+    const uint32_t step = 8 / std::gcd(a.kv_heads, 8u);
+    const uint32_t chunks = (min(a.k_pos_stride / 64, 32u) + step - 1) / step * step;
+    hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(a.heads * chunks), dim3(256), 0, stream, a, chunks);
+    hipLaunchKernelGGL(attn_values_kernel<HD>, dim3(a.heads * (HD / 32)), dim3(512), 0, stream, a);
     return (int)hipGetLastError();
 }
 

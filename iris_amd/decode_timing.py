@@ -254,6 +254,32 @@ def trace_decode(steps: int = 64) -> dict:
     return {"decode_ms_per_step": round(ms, 4), "prompt_pass_ms": round(prefill, 2), "steps": steps}
 
 
+def eager_decode(steps: int, gemma: bool = False) -> dict:
+    """A short decode with every launch issued from the host (no graph), for
+    kernel traces and counters: Mistral-7B shape after a 512-token prompt
+    (session of 1024 positions), or Gemma-2B shape after a 128-token prompt;
+    returns the wall time of the generate call."""
+    import time
+    if gemma:
+        g = GemmaDecodeBench(steps)
+        session, prompt = g.session, g.prompt
+    else:
+        model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
+        dm = DeviceModel(model)
+        del model.tensors
+        session, prompt = Session(dm, 1024, PROMPT), synth.token_ids(1, PROMPT, 32000)
+    t = time.time()
+    out = session.generate(prompt, steps, use_graph=False)
+    wall = time.time() - t
+    if gemma:
+        g.free()
+    else:
+        session.free()
+        dm.free()
+    return {"family": "gemma-dense" if gemma else "mistral-dense", "steps": steps, "tokens": len(out.token_ids),
+            "wall_s": round(wall, 3)}
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
     ap.add_argument("--steps", type=int, default=PROMPT - 1)
@@ -270,8 +296,15 @@ def main(argv=None):
                     help="only a short decode of STEPS steps (for kernel traces)")
     ap.add_argument("--gemma-2b", type=int, default=0, metavar="STEPS",
                     help="only the Gemma-2B-shape decode: a 128-token prompt and STEPS timed steps")
+    ap.add_argument("--eager-decode", type=int, default=0, metavar="STEPS",
+                    help="only a decode of STEPS steps launched from the host, no graph (for traces and "
+                         "counters); Mistral-7B shape, or Gemma-2B shape with --gemma")
+    ap.add_argument("--gemma", action="store_true", help="with --eager-decode: the Gemma-2B shape")
     args = ap.parse_args(argv)
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    if args.eager_decode:
+        print(json.dumps(eager_decode(args.eager_decode, args.gemma)), flush=True)
+        return
     if args.trace_decode:
         print(json.dumps(trace_decode(args.trace_decode)), flush=True)
         return
