@@ -184,7 +184,10 @@ void iris_model_free(IrisModel* model);
 uint64_t iris_model_device_bytes(const IrisModel* model);
 
 /* A KV cache for positions 0..max_positions and work space for passes of up
- * to max_rows rows. */
+ * to max_rows rows. max_positions is at most 65535 (-5 beyond: the
+ * matrix-core attention's exact value sums stay in int32 below 2^16 keys);
+ * the reference bounds a view only by the model's max_positions
+ * (crates/inference/kernels/src/mistral/layer.rs:121-127). */
 int iris_session_create(IrisModel* model, uint32_t max_positions, uint32_t max_rows, IrisSession** out);
 void iris_session_free(IrisSession* session);
 
