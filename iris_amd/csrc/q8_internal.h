@@ -120,9 +120,6 @@ struct GemvArgs {
     const int32_t* residual;
     uint32_t residual_stride;
     int32_t softcap;
-    // EPI_SWIGLU of the matrix-core products: the device's silu table
-    // (iris_silu_table); null computes each silu.
-    const int32_t* silu_tab;
     // EPI_ROPE_KV
     const int32_t* d_pos;       // absolute position of token 0 of this launch
     const int64_t* inv_freq;    // head_dim/2 Q32.32 angles per position
@@ -164,6 +161,9 @@ struct GemvArgs {
     const int32_t* res_in;
     int32_t res_scalar;         // 0 = none
     int32_t* res_out;
+    // EPI_SWIGLU of the matrix-core products: the device's silu table
+    // (iris_silu_table); null computes each silu.
+    const int32_t* silu_tab;
 };
 
 constexpr uint32_t GEMV_SSQ_SLOTS = 256;
