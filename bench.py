@@ -187,6 +187,12 @@ def main():
     bench.dm.free()
     gemm = decode_timing.time_gemm(TEACHER_FORCED_ROWS)
     log(f"MFMA GEMM {gemm['shape']}: {gemm['us']} us = {gemm['mfma_tops']} TOP/s ({100 * gemm['frac']:.1f}% of int8 peak)")
+    # The isolated product microbenchmark's GEMM: M=512, K=N=4096, row scales,
+    # activations a * s_t (a in [-127, 127], s_t = 2^8 + random % 2^8).
+    c2 = decode_timing.time_gemm(512, n=4096, k=4096, x=decode_timing.c2_activations())
+    c2["algorithmic_frac"] = round(c2["product_tops"] / decode_timing.INT8_PEAK_TOPS, 4)
+    log(f"C2 GEMM {c2['shape']}: {c2['us']} us, {c2['digit_planes']} digit planes = {c2['mfma_tops']} TOP/s issued "
+        f"({100 * c2['frac']:.1f}%), {c2['product_tops']} TOP/s algorithmic ({100 * c2['algorithmic_frac']:.1f}%)")
     gemm_pb = decode_timing.time_gemm(TEACHER_FORCED_ROWS, per_row_scale=False)
     log(f"MFMA GEMM per-block scales {gemm_pb['shape']}: {gemm_pb['us']} us, {gemm_pb['weight_planes']} weight planes "
         f"= {gemm_pb['mfma_tops']} TOP/s ({100 * gemm_pb['frac']:.1f}% of int8 peak)")
@@ -221,6 +227,7 @@ def main():
                    "prompt_tokens": PROMPT, "decode_steps_timed": args.steps, "batch": 1},
         "roofline": roof,
         "gemv_per_block": gemv_pb,
+        "c2_gemm": c2,
         "decode_roofline": {"bound": "hbm", "achieved": round(decode_gbps, 1), "peak": PEAK_HBM_GBPS,
                             "unit": "GB/s", "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
                             "bytes_per_token": int(per_token)},

@@ -393,38 +393,40 @@ __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint3
 // contiguous range, walked in bands of 8 row groups with the token groups
 // inside a band, so blocks in flight together share operands in their XCD's
 // L2.
-template <uint32_t W>
+template <uint32_t W, uint32_t TG>
 __global__ __launch_bounds__(64 * W, 1) void q8_gemm_row_kernel(const GemvArgs a) {
+    static_assert(TG == 2 || TG == 4, "64 or 128 tokens per workgroup");
     using G = GemmShape<W>;
     __shared__ __attribute__((aligned(1024))) int8_t smem[G::SMEM];
     int& s_limbs = *(int*)smem;  // read before the ring is first filled
     const uint32_t tid = threadIdx.x;
     const uint32_t TT = (a.tokens + 31) / 32;
-    const uint32_t n_rg = (a.w.tiles + 2 * G::RT - 1) / (2 * G::RT), n_tg = (TT + GM_TT - 1) / GM_TT;
+    const uint32_t n_rg = (a.w.tiles + 2 * G::RT - 1) / (2 * G::RT), n_tg = (TT + TG - 1) / TG;
     const uint32_t total = n_rg * n_tg;
     uint32_t b = blockIdx.x;
     if (total % 8 == 0) b = (b % 8) * (total / 8) + b / 8;
     const uint32_t band = b / (GM_BAND * n_tg), first = band * GM_BAND, rows_in_band = min(GM_BAND, n_rg - first);
     const uint32_t r = b - band * GM_BAND * n_tg;
-    const uint32_t rt0 = (first + r % rows_in_band) * G::RT, tt0 = (r / rows_in_band) * GM_TT;
+    const uint32_t rt0 = (first + r % rows_in_band) * G::RT, tt0 = (r / rows_in_band) * TG;
 
     if (tid == 0) s_limbs = 1;
     __syncthreads();
-    if (tid < GM_TT * 32 && tt0 * 32 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 32 + tid]);
+    if (tid < TG * 32 && tt0 * 32 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 32 + tid]);
     __syncthreads();
     const int limbs = s_limbs;
     __syncthreads();
+    constexpr int TTW = TG / 2;  // token tiles per wave for up to three planes
     switch (limbs) {
-        case 1: gemm_pass<G, 1, 2>(a, smem, rt0, tt0); break;
-        case 2: gemm_pass<G, 2, 2>(a, smem, rt0, tt0); break;
-        case 3: gemm_pass<G, 3, 2>(a, smem, rt0, tt0); break;
+        case 1: gemm_pass<G, 1, TTW>(a, smem, rt0, tt0); break;
+        case 2: gemm_pass<G, 2, TTW>(a, smem, rt0, tt0); break;
+        case 3: gemm_pass<G, 3, TTW>(a, smem, rt0, tt0); break;
         case 4:
             gemm_pass<G, 4, 1>(a, smem, rt0, tt0);
-            gemm_pass<G, 4, 1>(a, smem, rt0, tt0 + 2);
+            if constexpr (TG == 4) gemm_pass<G, 4, 1>(a, smem, rt0, tt0 + 2);
             break;
         default:
             gemm_pass<G, 5, 1>(a, smem, rt0, tt0);
-            gemm_pass<G, 5, 1>(a, smem, rt0, tt0 + 2);
+            if constexpr (TG == 4) gemm_pass<G, 5, 1>(a, smem, rt0, tt0 + 2);
             break;
     }
 }
@@ -703,14 +705,22 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
         }
         return (int)hipGetLastError();
     }
-    // Two waves per SIMD and 256 rows when that still gives every CU a
-    // workgroup, else one wave per SIMD and 128 rows.
-    const uint32_t n_tg = (TT + GM_TT - 1) / GM_TT;
+    // Two waves per SIMD and 256 rows x 128 tokens when that still gives
+    // every CU a workgroup, else one wave per SIMD and 128 rows, with 64
+    // tokens when the rounds of workgroups that gives cost less: a 64-token
+    // workgroup takes about 2/3 of a 128-token one's time (M=512, K=N=4096:
+    // 256 of them 60.6 us, 128 of the larger 92.1 us).
+    const uint32_t n_tg = (TT + GM_TT - 1) / GM_TT, n_tg2 = (TT + 1) / 2;
+    const uint32_t cus = (uint32_t)iris_device_cus();
     const uint32_t n8 = (a.w.tiles + 15) / 16 * n_tg, n4 = (a.w.tiles + 7) / 8 * n_tg;
-    if (n8 >= (uint32_t)iris_device_cus())
-        hipLaunchKernelGGL(q8_gemm_row_kernel<8>, dim3(n8), dim3(512), 0, stream, a);
+    const uint32_t n42 = (a.w.tiles + 7) / 8 * n_tg2;
+    const uint32_t rounds4 = (n4 + cus - 1) / cus, rounds2 = (n42 + cus - 1) / cus;
+    if (n8 >= cus)
+        hipLaunchKernelGGL((q8_gemm_row_kernel<8, 4>), dim3(n8), dim3(512), 0, stream, a);
+    else if (n42 != n4 && 2 * rounds2 <= 3 * rounds4)
+        hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2>), dim3(n42), dim3(256), 0, stream, a);
     else
-        hipLaunchKernelGGL(q8_gemm_row_kernel<4>, dim3(n4), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4>), dim3(n4), dim3(256), 0, stream, a);
     return (int)hipGetLastError();
 }
 

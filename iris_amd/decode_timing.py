@@ -76,8 +76,29 @@ def time_gemv(iterations: int = 200, n: int = GEMV_N, k: int = GEMV_K, per_row_s
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 
+def digit_planes_needed(x: np.ndarray, group: int = 128) -> np.ndarray:
+    """Signed byte digits each group of `group` tokens takes on the matrix
+    cores: the most any value of the group needs (the bytes of v +
+    0x8080808080, each xor 0x80; 1 to 5)."""
+    d = (x.astype(np.int64) + 0x8080808080).astype(np.uint64) ^ np.uint64(0x8080808080)
+    limbs = np.ones(d.shape, dtype=np.int64)
+    for sh in (8, 16, 24, 32):
+        limbs = np.maximum(limbs, np.where((d >> np.uint64(sh)) != 0, sh // 8 + 1, 1))
+    per_token = limbs.max(axis=1)
+    return np.array([per_token[i:i + group].max() for i in range(0, len(per_token), group)])
+
+
+def c2_activations(tokens: int = 512, k: int = GEMV_K, seed: int = 5) -> np.ndarray:
+    """The isolated product's activations: a * s_t with a uniform in
+    [-127, 127] and a per-token Q16.16 integer s_t = 2^8 + (random % 2^8)."""
+    rng = np.random.default_rng(seed)
+    a = rng.integers(-127, 128, (tokens, k)).astype(np.int64)
+    s_t = (256 + rng.integers(0, 256, (tokens, 1))).astype(np.int64)
+    return (a * s_t).astype(np.int32)
+
+
 def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iterations: int = 20,
-              magnitude_bits: int = 21, per_row_scale: bool = True) -> dict:
+              magnitude_bits: int = 21, per_row_scale: bool = True, x=None) -> dict:
     """Average duration of one multi-token Q8_0 product on the int8 matrix
     cores (digit planes + MFMA GEMM) at the gate|up shape of the 2048-row
     pass, with activations of `magnitude_bits` bits (three signed byte
@@ -90,10 +111,11 @@ def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iteration
 
     raw = synth.q8_matrix(synth.tensor_seed(3, 1), n, k, synth.scale_base_for(k), per_row_scale)
     m = Q8Matrix.from_bytes(raw, n, k)
-    rng = np.random.default_rng(4)
-    half = 1 << (magnitude_bits - 1)
-    x = rng.integers(-half, half, (tokens, k)).astype(np.int32)
-    dx = native.DeviceBuffer.from_array(x)
+    if x is None:
+        rng = np.random.default_rng(4)
+        half = 1 << (magnitude_bits - 1)
+        x = rng.integers(-half, half, (tokens, k)).astype(np.int32)
+    dx = native.DeviceBuffer.from_array(np.ascontiguousarray(x, dtype=np.int32))
     dout = native.DeviceBuffer(tokens * n * 4)
     L = native.lib()
     ws_bytes = L.q8gpu_workspace_bytes(m.handle, tokens)
@@ -103,12 +125,15 @@ def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iteration
                                         C.byref(ms)), "time GEMM")
     info = m.info()
     m.free()
-    digits = 3 if magnitude_bits <= 24 else 4
+    # digit planes of each 128-token group (as the launch takes them)
+    groups = digit_planes_needed(x)
+    sizes = np.minimum(128, tokens - 128 * np.arange(len(groups)))
+    digits = int(groups.max())
     # weight digit planes: 1 for a row-scale matrix; a folded one holds
     # (device bytes - int8 weights - f16 scales - row shifts) / int8 weights
     qs = n * k
     wplanes = 1 if per_row_scale else round((info["bytes"] - qs - n * k // 32 * 2 - 4 * ((n + 15) // 16 * 16)) / qs)
-    ops = 2.0 * tokens * n * k * digits * wplanes
+    ops = 2.0 * float((groups * sizes).sum()) * n * k * wplanes
     tops = ops / (ms.value * 1e-3) / 1e12
     return {"shape": f"M={tokens} K={k} N={n}", "scales": "per row" if per_row_scale else "per block (folded)",
             "us": round(ms.value * 1e3, 1), "digit_planes": digits, "weight_planes": wplanes,
