@@ -20,6 +20,9 @@ The JSON line also carries:
   checkpoints) and its gate|up product (M=2048, K=4096, N=28672) on the
   int8 matrix cores, against the 5.0 POP/s dense int8 peak (the executed
   MFMA work counts each signed byte digit plane of the activations);
+- pcie_inclusive: the drop-in entry point q8gpu_product (host buffers in
+  and out of every call, as the reference's gpu.rs calls it) timed per call
+  for the microbenchmark's GEMV and GEMM, the matrix already uploaded;
 - cpu_baseline: the CPU oracle (a C restatement of the reference's kernels)
   timed on a bounded sample of the same decode on this host's cores.
 """
@@ -43,7 +46,7 @@ PEAK_HBM_GBPS = 8000.0
 # and WRITE_SIZE passes scaled by a 256 MiB device copy (fetch x2.000, write
 # x1.000): profiles/q8_gemv_row_scale_k4096_n14336.md. Re-measure when the
 # kernel or its layout changes.
-GEMV_TRAFFIC_BYTES = 59_357_000
+GEMV_TRAFFIC_BYTES = 59_372_000
 PROMPT = 512  # the prompt length of the timed workload
 DECODE_TOKENS = 512
 TEACHER_FORCED_ROWS = 2048
@@ -193,6 +196,14 @@ def main():
     c2["algorithmic_frac"] = round(c2["product_tops"] / decode_timing.INT8_PEAK_TOPS, 4)
     log(f"C2 GEMM {c2['shape']}: {c2['us']} us, {c2['digit_planes']} digit planes = {c2['mfma_tops']} TOP/s issued "
         f"({100 * c2['frac']:.1f}%), {c2['product_tops']} TOP/s algorithmic ({100 * c2['algorithmic_frac']:.1f}%)")
+    # The drop-in entry point's PCIe-inclusive rate (host buffers in and out
+    # of every call), for both microbenchmark products.
+    host_gemv = decode_timing.time_host_product(1)
+    host_gemm = decode_timing.time_host_product(512, n=4096, k=4096, x=decode_timing.c2_activations())
+    pcie = {"entry_point": "q8gpu_product (host activations in, host outputs out, synchronous)",
+            "gemv_us": host_gemv["us"], "gemm_us": host_gemm["us"], "gemv_shape": "M=1 K=4096 N=14336",
+            "gemm_shape": "M=512 K=4096 N=4096", "gemm_host_bytes": host_gemm["host_bytes"]}
+    log(f"q8gpu_product with host buffers: GEMV {host_gemv['us']} us per call, GEMM M=512 {host_gemm['us']} us")
     gemm_pb = decode_timing.time_gemm(TEACHER_FORCED_ROWS, per_row_scale=False)
     log(f"MFMA GEMM per-block scales {gemm_pb['shape']}: {gemm_pb['us']} us, {gemm_pb['weight_planes']} weight planes "
         f"= {gemm_pb['mfma_tops']} TOP/s ({100 * gemm_pb['frac']:.1f}% of int8 peak)")
@@ -228,6 +239,7 @@ def main():
         "roofline": roof,
         "gemv_per_block": gemv_pb,
         "c2_gemm": c2,
+        "pcie_inclusive": pcie,
         "decode_roofline": {"bound": "hbm", "achieved": round(decode_gbps, 1), "peak": PEAK_HBM_GBPS,
                             "unit": "GB/s", "frac": round(decode_gbps / PEAK_HBM_GBPS, 4),
                             "bytes_per_token": int(per_token)},

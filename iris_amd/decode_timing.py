@@ -73,6 +73,31 @@ def time_gemv(iterations: int = 200, n: int = GEMV_N, k: int = GEMV_K, per_row_s
             "algorithmic_bytes": gemv_algorithmic_bytes(n, k)}
 
 
+def time_host_product(tokens: int, n: int = GEMV_N, k: int = GEMV_K, iterations: int = 20,
+                      x: np.ndarray | None = None) -> dict:
+    """Wall time per call of the drop-in entry point q8gpu_product (host
+    activations in, host outputs out, synchronous: the calls the reference's
+    gpu.rs makes), the matrix (one f16 scale per row) already on the device,
+    after one untimed call that sizes the library's device arena: the
+    PCIe-inclusive rate of a product."""
+    import time
+    from .tensor import Q8Matrix, linear_slab_from_source
+
+    raw = synth.q8_matrix(synth.tensor_seed(2, 1), n, k, synth.scale_base_for(k), True)
+    m = Q8Matrix.from_bytes(raw, n, k)
+    if x is None:
+        rng = np.random.default_rng(2)
+        x = (rng.integers(-127, 128, (tokens, k)) * (256 + int(rng.integers(0, 256)))).astype(np.int32)
+    linear_slab_from_source(x, m)
+    t0 = time.perf_counter()
+    for _ in range(iterations):
+        linear_slab_from_source(x, m)
+    us = (time.perf_counter() - t0) / iterations * 1e6
+    m.free()
+    return {"us": round(us, 1), "tokens": tokens, "n": n, "k": k,
+            "host_bytes": int(tokens * k * 4 + tokens * n * 4), "calls": iterations}
+
+
 INT8_PEAK_TOPS = 5000.0  # MI355X dense int8 MFMA
 
 
