@@ -276,7 +276,7 @@ int q8gpu_product_device(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t to
 
 uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* m, uint32_t tokens) {
     if (!m || tokens < 2) return 0;
-    return planes_bytes(m->cols, tokens) + 8ull * tokens;
+    return planes_bytes(m->cols, tokens) + 4ull * gemm_limb_ints(m->cols, tokens);
 }
 
 }  // extern "C"

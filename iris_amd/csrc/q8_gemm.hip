@@ -68,13 +68,13 @@ __device__ __forceinline__ uint32_t plane_byte4(uint64_t d0, uint64_t d1, uint64
            ((uint32_t)((d3 >> sh) & 0xff) << 24);
 }
 
-// Per token, one wave each: the digit count reset to one and, under the
-// rms_norm prologue, the token's scale (ops.rs:98-114, rms_norm_scale of the
-// order-free saturating sum of squares) at token_limbs[tokens + t].
+// Per token, one wave each, under the rms_norm prologue only: the token's
+// scale (ops.rs:98-114, rms_norm_scale of the order-free saturating sum of
+// squares) at token_limbs[t].
 __global__ __launch_bounds__(256) void token_prep_kernel(const GemvArgs a) {
     const uint32_t t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
     if (t >= a.tokens) return;
-    if (a.prologue == PRO_RMSNORM) {
+    {
         const uint32_t K = a.w.cols;
         const int32_t* x = a.x + (size_t)t * a.x_stride;
         int64_t s = 0;
@@ -86,30 +86,31 @@ __global__ __launch_bounds__(256) void token_prep_kernel(const GemvArgs a) {
             s = dn::acc_add_sat(s, (int64_t)v.w * v.w);
         }
         for (int off = 32; off >= 1; off >>= 1) s = dn::acc_add_sat(s, __shfl_xor(s, off));
-        if (lane == 0) a.token_limbs[a.tokens + t] = dn::rms_scale_from_sum(s, K, a.norm_eps);
+        if (lane == 0) a.token_limbs[t] = dn::rms_scale_from_sum(s, K, a.norm_eps);
     }
-    if (lane == 0) a.token_limbs[t] = 1;
 }
 
-constexpr uint32_t PLANE_KB = 16;  // 32-wide k blocks per digit-plane workgroup
+constexpr uint32_t PLANE_KB = GEMM_PLANE_KB;
 
-// The digit planes of one 32-token tile over PLANE_KB k blocks per
-// workgroup, after the optional rms_norm (mul_sat(mul_sat(v, scale), w)),
-// in the operand layout above; each token's digit count is raised to what
-// these values need. Tokens past the end of the last tile get zero digits.
+// The digit planes of one 32-token tile over PLANE_KB k blocks (one k
+// chunk) per workgroup, after the optional rms_norm (mul_sat(mul_sat(v,
+// scale), w)), in the operand layout above, and the digits the chunk's
+// values need, stored for the (chunk, tile) at token_limbs[M + chunk * TT +
+// tile]: every launch writes each of its counts, so none needs a reset.
+// Tokens past the end of the last tile get zero digits.
 __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
-    __shared__ int s_need[32];
+    __shared__ int s_need;
     const uint32_t tt = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t K = a.w.cols, M = a.tokens, TT = (M + 31) / 32, KB = K / 32;
     const uint32_t kb0 = blockIdx.y * PLANE_KB, kb1 = min(kb0 + PLANE_KB, KB);
     const bool norm = a.prologue == PRO_RMSNORM;
-    if (tid < 32) s_need[tid] = 1;
+    if (tid == 0) s_need = 1;
     __syncthreads();
     // Lane l writes the 16 bytes of token l % 32 at k-offset 16 * (l / 32)
     // of each 32-wide block the wave takes.
     const uint32_t tl = lane & 31, q = lane >> 5, t = tt * 32 + tl;
     const bool valid = t < M;
-    const int32_t scale = norm && valid ? a.token_limbs[M + t] : 0;
+    const int32_t scale = norm && valid ? a.token_limbs[t] : 0;
     const int32_t* x = a.x + (size_t)(valid ? t : 0) * a.x_stride;
     const size_t lstride = (size_t)TT * KB * FRAG;
     int need = 1;
@@ -137,10 +138,28 @@ __global__ __launch_bounds__(256) void digit_planes_kernel(const GemvArgs a) {
         for (int l = 0; l < PL_MAX; l++)
             *(uint4*)(dst + l * lstride) = make_uint4(out[l][0], out[l][1], out[l][2], out[l][3]);
     }
-    need = max(need, __shfl_xor(need, 32));
-    if (lane < 32) atomicMax(&s_need[lane], need);
+    for (int off = 32; off >= 1; off >>= 1) need = max(need, __shfl_xor(need, off));
+    if (lane == 0) atomicMax(&s_need, need);  // the largest of four: any order
     __syncthreads();
-    if (tid < 32 && tt * 32 + tid < M && s_need[tid] > 1) atomicMax(&a.token_limbs[tt * 32 + tid], s_need[tid]);
+    if (tid == 0) a.token_limbs[M + blockIdx.y * TT + tt] = s_need;
+}
+
+// The digits a workgroup's token tiles tt0 .. tt0 + tg - 1 need: the most
+// any k chunk of them needs, from digit_planes_kernel's counts.
+__device__ __forceinline__ int tiles_limbs(const GemvArgs& a, uint32_t tt0, uint32_t tg, int& s_limbs) {
+    const uint32_t tid = threadIdx.x, TT = (a.tokens + 31) / 32;
+    const uint32_t chunks = (a.w.cols / 32 + PLANE_KB - 1) / PLANE_KB;
+    const int32_t* need = a.token_limbs + a.tokens;
+    if (tid == 0) s_limbs = 1;
+    __syncthreads();
+    for (uint32_t i = tid; i < tg * chunks; i += blockDim.x) {
+        const uint32_t t = tt0 + i % tg;
+        if (t < TT) atomicMax(&s_limbs, need[(i / tg) * TT + t]);
+    }
+    __syncthreads();
+    const int limbs = s_limbs;
+    __syncthreads();
+    return limbs;
 }
 
 template <int N>
@@ -409,12 +428,7 @@ __global__ __launch_bounds__(64 * W, 1) void q8_gemm_row_kernel(const GemvArgs a
     const uint32_t r = b - band * GM_BAND * n_tg;
     const uint32_t rt0 = (first + r % rows_in_band) * G::RT, tt0 = (r / rows_in_band) * TG;
 
-    if (tid == 0) s_limbs = 1;
-    __syncthreads();
-    if (tid < TG * 32 && tt0 * 32 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 32 + tid]);
-    __syncthreads();
-    const int limbs = s_limbs;
-    __syncthreads();
+    const int limbs = tiles_limbs(a, tt0, TG, s_limbs);
     constexpr int TTW = TG / 2;  // token tiles per wave for up to three planes
     switch (limbs) {
         case 1: gemm_pass<G, 1, TTW>(a, smem, rt0, tt0); break;
@@ -657,12 +671,7 @@ __global__ __launch_bounds__(256, 1) void q8_gemm_fold_kernel(const GemvArgs a) 
     const uint32_t band = b / (GM_BAND * n_tg), first = band * GM_BAND, rows_in_band = min(GM_BAND, n_rg - first);
     const uint32_t r = b - band * GM_BAND * n_tg;
     const uint32_t rt0 = (first + r % rows_in_band) * RT, tt0 = (r / rows_in_band) * TG;
-    if (tid == 0) s_limbs = 1;
-    __syncthreads();
-    if (tid < TG * 32 && tt0 * 32 + tid < a.tokens) atomicMax(&s_limbs, a.token_limbs[tt0 * 32 + tid]);
-    __syncthreads();
-    const int limbs = s_limbs;
-    __syncthreads();
+    const int limbs = tiles_limbs(a, tt0, TG, s_limbs);
     switch (limbs) {
         case 1: fold_pass<WP, 1>(a, smem, rt0, tt0); break;
         case 2: fold_pass<WP, 2>(a, smem, rt0, tt0); break;
@@ -689,7 +698,8 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
         return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
     const uint32_t TT = (a.tokens + 31) / 32, KB = a.w.cols / 32;
-    hipLaunchKernelGGL(token_prep_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
+    if (a.prologue == PRO_RMSNORM)
+        hipLaunchKernelGGL(token_prep_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
     hipLaunchKernelGGL(digit_planes_kernel, dim3(TT, (KB + PLANE_KB - 1) / PLANE_KB), dim3(256), 0, stream, a);
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return (int)st;

@@ -145,7 +145,8 @@ struct GemvArgs {
     // Multi-token products of row-scale matrices go through the int8 MFMA
     // GEMM when this work space is given (null: the GEMV path).
     int8_t* planes;             // gemm_planes_bytes(cols, tokens): 5 digit planes, MFMA-operand tiled
-    int32_t* token_limbs;       // [2][tokens]: digits each token's activations need, then its rms_norm scale
+    int32_t* token_limbs;       // gemm_limb_ints(cols, tokens): each token's rms_norm scale, then the digits
+                                // each (k chunk, 32-token tile) of the activations needs, [chunk][tile]
     // One-token launches only. ssq_out (EPI_RESIDUAL or EPI_STORE): each
     // tile's saturating sum of the squares of its outputs, slot [tile].
     // ssq_in (PRO_RMSNORM, PRO_NORM_RES_NORM: the first norm):
@@ -178,6 +179,15 @@ __device__ __forceinline__ void lds_barrier() {
 // up to whole 32-token tiles, times cols, 256-byte aligned.
 inline uint64_t gemm_planes_bytes(uint32_t cols, uint32_t tokens) {
     return (5ull * ((tokens + 31ull) & ~31ull) * cols + 255) & ~255ull;
+}
+
+constexpr uint32_t GEMM_PLANE_KB = 8;  // 32-wide k blocks per digit-plane workgroup (one k chunk)
+
+// The ints of token_limbs a multi-token product uses: one rms_norm scale per
+// token, then one digit count per (k chunk, 32-token tile).
+inline uint64_t gemm_limb_ints(uint32_t cols, uint32_t tokens) {
+    const uint64_t chunks = ((uint64_t)cols / 32 + GEMM_PLANE_KB - 1) / GEMM_PLANE_KB;
+    return tokens + chunks * ((tokens + 31ull) / 32);
 }
 
 // The MFMA GEMM for a multi-token product (row-scale matrix, planes set);

@@ -988,7 +988,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
         if (d.family != IRIS_FAMILY_GEMMA_DENSE && st == hipSuccess) st = (hipError_t)iris_silu_table(&s->silu_tab);
         size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
         if (st == hipSuccess) st = hipMalloc((void**)&s->planes, gemm_planes_bytes((uint32_t)widest, max_rows));
-        alloc(&s->token_limbs, 2 * (size_t)max_rows);
+        alloc(&s->token_limbs, (size_t)gemm_limb_ints((uint32_t)widest, max_rows));
         AttnPlanes& ap = s->attn_planes;
         ap.qt_cap = (max_rows + 15) / 16;
         ap.ks_cap = (max_positions + 63) / 64;

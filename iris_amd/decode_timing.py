@@ -340,6 +340,8 @@ def main(argv=None):
     ap.add_argument("--pass-rows", type=int, default=0,
                     help="time only the teacher-forced pass over this many rows")
     ap.add_argument("--gemm-only", action="store_true", help="time only the MFMA product at the gate|up shape")
+    ap.add_argument("--c2-gemm", action="store_true",
+                    help="time only the isolated product's GEMM (M=512, K=N=4096, row scales)")
     ap.add_argument("--per-block", action="store_true",
                     help="with --gemm-only, --gemv-only or --pass-rows: per-block scale matrices")
     ap.add_argument("--trace-decode", type=int, default=0, metavar="STEPS",
@@ -367,6 +369,9 @@ def main(argv=None):
                           "prompt_pass_ms": round(prefill, 2), "bytes_per_step": int(b),
                           "achieved_gbps": round(b / (ms * 1e-3) / 1e9, 1)}), flush=True)
         g.free()
+        return
+    if args.c2_gemm:
+        print(json.dumps(time_gemm(512, n=4096, k=GEMV_K, x=c2_activations())), flush=True)
         return
     if args.gemm_only:
         print(json.dumps(time_gemm(per_row_scale=not args.per_block)), flush=True)
