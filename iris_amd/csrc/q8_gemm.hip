@@ -44,14 +44,22 @@ constexpr uint32_t GM_BAND = 8;             // row groups per band of the launch
 // 128 tokens (W = 8: two waves per SIMD, 256 rows, for launches that fill
 // the chip; W = 4: one wave per SIMD, 128 rows, for smaller ones). A stage
 // is one 64-wide k step: 2W weight operands and up to 24 digit-plane ones.
-template <uint32_t W>
+//
+// SPLIT = 2 (four-wave shape only): the workgroup holds two such groups of
+// W waves (two waves per SIMD), each walking half of the k steps through a
+// two-stage ring of its own; the second group's int32 plane sums are then
+// added into the first's (exact: the whole row's sum fits int32), and both
+// groups store the block.
+template <uint32_t W, uint32_t SPLIT = 1>
 struct GemmShape {
-    static constexpr uint32_t WAVES = W, THREADS = 64 * W, RT = W;  // RT: 32-row tiles
+    static constexpr uint32_t WAVES = W, RT = W;                     // per k group; RT: 32-row tiles
+    static constexpr uint32_t SPLITS = SPLIT, THREADS = 64 * W * SPLIT;
     static constexpr int RI = 2;                                      // row tiles per wave
     static constexpr uint32_t STAGE = (2 * W + 24) * FRAG;
-    static constexpr uint32_t STAGES = W == 8 ? 3 : 4;
+    static constexpr uint32_t STAGES = SPLIT == 2 ? 2 : W == 8 ? 3 : 4;
+    static constexpr uint32_t RING = STAGES * STAGE;                  // per k group
     static constexpr uint32_t OUT = 32 * W * 129 * 4;  // the output block, [row][128 tokens + 1]
-    static constexpr uint32_t SMEM = STAGES * STAGE > OUT ? STAGES * STAGE : OUT;
+    static constexpr uint32_t SMEM = SPLIT * RING > OUT ? SPLIT * RING : OUT;
 };
 
 __device__ __forceinline__ uint64_t digits5(int32_t v) {
@@ -184,10 +192,14 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
     constexpr uint32_t PER_WAVE = (CHUNKS + G::WAVES - 1) / G::WAVES;
     constexpr uint32_t GM_RT = G::RT, GM_STAGES = G::STAGES, GM_STAGE = G::STAGE;
     static_assert(PER_WAVE * G::WAVES * FRAG <= G::STAGE && PER_WAVE >= 2, "stage layout");
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    // The wave within its k group, the group's ring and k steps [ks0, ks1).
+    const uint32_t half = (tid >> 6) / G::WAVES, wave = (tid >> 6) % G::WAVES;
     const uint32_t wr = wave % (G::WAVES / 2), wt = wave / (G::WAVES / 2);
     const Q8View& w = a.w;
     const uint32_t KS = w.cols / 64, KB = w.cols / 32, TT = (a.tokens + 31) / 32;
+    const uint32_t ks0 = half * (KS / G::SPLITS), ks1 = ks0 + KS / G::SPLITS;
+    smem += half * G::RING;
     const size_t lstride = (size_t)TT * KB * FRAG;
 
     // Wave w copies chunks w, w + W, ...: the first two are weight operands
@@ -220,16 +232,19 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
 
 #pragma unroll
     for (uint32_t s = 0; s < GM_STAGES - 1; s++)
-        if (s < KS) issue(s);
-    for (uint32_t ks = 0; ks < KS; ks++) {
+        if (ks0 + s < ks1) issue(ks0 + s);
+    // Both k groups take the same number of steps (the launcher's even KS),
+    // so their barriers pair up.
+    for (uint32_t ks = ks0; ks < ks1; ks++) {
         // This wave's copies for step ks are in LDS once at most the later
         // steps' copies are outstanding; the barrier makes every wave's
         // visible and frees the slot the next copy overwrites (read at ks-1).
-        if (GM_STAGES >= 4 && ks + 2 < KS) wait_vmem<(GM_STAGES >= 4 ? 2 : 1) * PER_WAVE>();
-        else if (ks + 1 < KS) wait_vmem<PER_WAVE>();
+        if (GM_STAGES == 2) wait_vmem<0>();
+        else if (GM_STAGES >= 4 && ks + 2 < ks1) wait_vmem<(GM_STAGES >= 4 ? 2 : 1) * PER_WAVE>();
+        else if (ks + 1 < ks1) wait_vmem<PER_WAVE>();
         else wait_vmem<0>();
         lds_barrier();
-        if (ks + GM_STAGES - 1 < KS) issue(ks + GM_STAGES - 1);
+        if (ks + GM_STAGES - 1 < ks1) issue(ks + GM_STAGES - 1);
         const int8_t* st = smem + (ks % GM_STAGES) * GM_STAGE + lane * 16;
 #pragma unroll
         for (uint32_t sub = 0; sub < 2; sub++) {
@@ -272,6 +287,7 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
     int32_t* sC = (int32_t*)smem;
 #pragma unroll
     for (int i = 0; i < G::RI; i++) {
+        if (wave >= G::WAVES) break;  // a second k group's sums are in the first's
 #pragma unroll
         for (int j = 0; j < TTW; j++) {
             const uint32_t tl = (wt * TTW + j) * 32 + (lane & 31);
@@ -402,6 +418,36 @@ __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint3
 #pragma unroll
             for (int l = 0; l < LG; l++) acc[i][j][l] = v16i{};
     gemm_mainloop<G, LG, TTW>(a, smem, rt0, tt0, acc);
+    if constexpr (G::SPLITS == 2) {
+        // The second k group's sums into the first's, one row tile at a
+        // time through LDS (TTW * LG * 16 KB each), lane-contiguous.
+        const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, hw = wave % G::WAVES;
+        static_assert(G::WAVES * TTW * LG * 16 * 64 * 4 <= G::SMEM, "combine fits the LDS");
+        int32_t* buf = (int32_t*)smem;
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            if (wave >= G::WAVES) {
+#pragma unroll
+                for (int j = 0; j < TTW; j++)
+#pragma unroll
+                    for (int l = 0; l < LG; l++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            buf[(((hw * TTW + j) * LG + l) * 16 + e) * 64 + lane] = acc[i][j][l][e];
+            }
+            lds_barrier();
+            if (wave < G::WAVES) {
+#pragma unroll
+                for (int j = 0; j < TTW; j++)
+#pragma unroll
+                    for (int l = 0; l < LG; l++)
+#pragma unroll
+                        for (int e = 0; e < 16; e++)
+                            acc[i][j][l][e] += buf[(((hw * TTW + j) * LG + l) * 16 + e) * 64 + lane];
+            }
+            lds_barrier();
+        }
+    }
     gemm_epilogue<G, LG, TTW>(a, smem, rt0, tt0, acc);
 }
 
@@ -412,10 +458,10 @@ __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint3
 // contiguous range, walked in bands of 8 row groups with the token groups
 // inside a band, so blocks in flight together share operands in their XCD's
 // L2.
-template <uint32_t W, uint32_t TG>
-__global__ __launch_bounds__(64 * W, 1) void q8_gemm_row_kernel(const GemvArgs a) {
+template <uint32_t W, uint32_t TG, uint32_t SPLIT = 1>
+__global__ __launch_bounds__(64 * W * SPLIT, 1) void q8_gemm_row_kernel(const GemvArgs a) {
     static_assert(TG == 2 || TG == 4, "64 or 128 tokens per workgroup");
-    using G = GemmShape<W>;
+    using G = GemmShape<W, SPLIT>;
     __shared__ __attribute__((aligned(1024))) int8_t smem[G::SMEM];
     int& s_limbs = *(int*)smem;  // read before the ring is first filled
     const uint32_t tid = threadIdx.x;
@@ -725,12 +771,18 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     const uint32_t n8 = (a.w.tiles + 15) / 16 * n_tg, n4 = (a.w.tiles + 7) / 8 * n_tg;
     const uint32_t n42 = (a.w.tiles + 7) / 8 * n_tg2;
     const uint32_t rounds4 = (n4 + cus - 1) / cus, rounds2 = (n42 + cus - 1) / cus;
+    // The four-wave shapes split the k steps between two wave groups when
+    // there is an even number of them (both groups' barriers pair up).
+    const bool split = (a.w.cols / 64) % 2 == 0;
     if (n8 >= cus)
         hipLaunchKernelGGL((q8_gemm_row_kernel<8, 4>), dim3(n8), dim3(512), 0, stream, a);
-    else if (n42 != n4 && 2 * rounds2 <= 3 * rounds4)
-        hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2>), dim3(n42), dim3(256), 0, stream, a);
-    else
-        hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4>), dim3(n4), dim3(256), 0, stream, a);
+    else if (n42 != n4 && 2 * rounds2 <= 3 * rounds4) {
+        if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2, 2>), dim3(n42), dim3(512), 0, stream, a);
+        else hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2>), dim3(n42), dim3(256), 0, stream, a);
+    } else {
+        if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4, 2>), dim3(n4), dim3(512), 0, stream, a);
+        else hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4>), dim3(n4), dim3(256), 0, stream, a);
+    }
     return (int)hipGetLastError();
 }
 
