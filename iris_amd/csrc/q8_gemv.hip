@@ -476,6 +476,68 @@ __device__ __forceinline__ int stage_row(const GemvArgs& a, const int32_t* x, ui
     return need;
 }
 
+// The persistent kernel's prologue staged by each wave on its own (PRO_NONE,
+// or PRO_RMSNORM from the producer's slots). A wave's blocks are
+// tile_blocks' slots part * 4 + g of nslots: the runs of four consecutive
+// blocks starting at part * 4 + j * nslots, 32 plane dwords each. The wave
+// stages the digit planes of those dwords only, at their places in planes,
+// and returns the digits its own values need: no wave waits for another's
+// row, and the digit count may differ between waves (the digits of a value
+// do not depend on how many are kept). Waves of one part write the same
+// values to the same places. issue() runs right after the first round's
+// row loads are issued, as in stage_row.
+template <int PRO, typename Issue>
+__device__ __forceinline__ int stage_wave(const GemvArgs& a, const int32_t* x, uint32_t pw, uint32_t* planes,
+                                          uint32_t part, uint32_t nslots, uint32_t lane, Issue&& issue) {
+    constexpr bool NORM = PRO == PRO_RMSNORM;
+    const int4* x4 = (const int4*)x;
+    const int4* n4 = (const int4*)a.norm_w;
+    const uint32_t span = nslots * 8, first = part * 32;
+    const uint32_t runs = first < pw ? (pw - first + span - 1) / span : 0;
+    const uint32_t n = runs * 32;  // the wave's dwords, some of the last run past the row
+    auto at = [&](uint32_t q) { return first + (q >> 5) * span + (q & 31); };
+    int4 v[XROUND], nw[XROUND];
+    auto load_round = [&](uint32_t q0) {
+#pragma unroll
+        for (uint32_t u = 0; u < XROUND; u++) {
+            const uint32_t q = q0 + 64 * u + lane;
+            const uint32_t i = q < n ? min(at(q), pw - 1) : pw - 1;
+            v[u] = x4[i];
+            nw[u] = NORM ? n4[i] : make_int4(0, 0, 0, 0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    load_round(0);
+    constexpr uint32_t SPL = GEMV_SSQ_SLOTS / 64;
+    int64_t sl[SPL];
+    if constexpr (NORM) {
+#pragma unroll
+        for (uint32_t u = 0; u < SPL; u++) sl[u] = a.ssq_in[min(lane + 64 * u, a.ssq_n - 1)];
+    }
+    issue();
+    int32_t scale = 0;
+    if constexpr (NORM) {
+        int64_t t = 0;
+#pragma unroll
+        for (uint32_t u = 0; u < SPL; u++)
+            if (lane + 64 * u < a.ssq_n) t = dn::acc_add_sat(t, sl[u]);
+        scale = dn::rms_scale_from_sum(wave_sum_sat_nonneg(t), pw * 4, a.norm_eps);
+    }
+    int need = 1;
+    for (uint32_t q0 = 0;;) {
+#pragma unroll
+        for (uint32_t u = 0; u < XROUND; u++) {
+            const uint32_t q = q0 + 64 * u + lane;
+            const uint32_t i = at(q);
+            if (q < n && i < pw) need = max(need, stage_int4(v[u], NORM, nw[u], scale, i, planes, pw));
+        }
+        q0 += 64 * XROUND;
+        if (q0 >= n) break;
+        load_round(q0);
+    }
+    return need;
+}
+
 // One block's contribution to the lane's accumulator (L digit planes,
 // uniform over the wave).
 template <int MODE>
@@ -663,7 +725,7 @@ __global__ __launch_bounds__(GEMV_THREADS) void q8_gemv_kernel(const GemvArgs a)
 // tile per CU, so that its few tiles still keep every wave slot busy.
 template <int MODE, int W, int PRO>
 __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a, const uint32_t split,
-                                                                 const uint32_t ahead) {
+                                                                 const uint32_t ahead, const uint32_t wave_stage) {
     extern __shared__ __align__(16) uint32_t planes[];  // MAX_LIMBS planes of K/4 dwords
     __shared__ dn::i128 red[W][Q8_TILE_ROWS];
     __shared__ TileIn s_in[W * Q8_TILE_ROWS];  // the first group's epilogue inputs, by tile and row
@@ -715,14 +777,24 @@ __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a
                                     tid % nin);
     };
 
-    // Once per workgroup: the norm scale and every digit plane of the row.
-    const int need = stage_row<W * 64, PRO>(a, x, pw, planes, ssq, tid, issue);
-    const int wave_need = wave_max_int(need);
-    if (lane == 0) s_need[wave] = wave_need;
-    lds_barrier();
-    int limbs = s_need[0];
+    // Once per workgroup: the norm scale and every digit plane of the row;
+    // or (wave_stage) each wave's own blocks' planes, staged by the wave.
+    int limbs;
+    if (PRO != PRO_NORM_RES_NORM && wave_stage) {
+        limbs = wave_max_int(stage_wave<PRO>(a, x, pw, planes, part, nslots, lane, issue));
+        // The wave reads only what its own lanes wrote: LDS keeps one wave's
+        // accesses in order, the fence keeps the compiler from moving them.
+        __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+    } else {
+        const int need = stage_row<W * 64, PRO>(a, x, pw, planes, ssq, tid, issue);
+        const int wave_need = wave_max_int(need);
+        if (lane == 0) s_need[wave] = wave_need;
+        lds_barrier();
+        limbs = s_need[0];
 #pragma unroll
-    for (int i = 1; i < W; i++) limbs = max(limbs, s_need[i]);
+        for (int i = 1; i < W; i++) limbs = max(limbs, s_need[i]);
+    }
 
     // One group of tiles; the first group is the workgroup's own (its
     // weights and epilogue inputs already issued), further ones (more groups
@@ -814,6 +886,7 @@ constexpr uint32_t WGS_PER_CU = 2;
 int g_num_cus = 0;
 uint32_t g_split_override = 0;
 uint32_t g_ahead_override = 0;  // weight batches issued before the row staging (1 or 2)
+uint32_t g_wave_stage = 1;      // 0: workgroup staging; 1: per-wave where each part has one wave; 2: wherever it applies
 
 void gemv_prepare_once() {
     static bool done = false;
@@ -835,6 +908,7 @@ void gemv_prepare_once() {
 #undef IRIS_PERSISTENT_W
     if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
     if (const char* e = getenv("IRIS_GEMV_AHEAD")) g_ahead_override = (uint32_t)atoi(e) == 1 ? 1 : 2;
+    if (const char* e = getenv("IRIS_GEMV_WAVE_STAGE")) g_wave_stage = (uint32_t)atoi(e) > 2 ? 2 : (uint32_t)atoi(e);
 }
 
 // Waves sharing one tile (of a workgroup's W): the most that still give a
@@ -874,11 +948,16 @@ int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) 
     const uint32_t wgs = min(groups, (uint32_t)resident);
     const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
     const uint32_t ahead = g_ahead_override ? g_ahead_override : 1;
+    // Each wave stages its own blocks' planes when the prologue allows it
+    // (no norm, or a norm from the producer's slots).
+    const bool eligible = a.prologue == PRO_NONE || (a.prologue == PRO_RMSNORM && a.ssq_in != nullptr);
+    const uint32_t wave_stage = eligible && (g_wave_stage == 2 || (g_wave_stage == 1 && split == W)) ? 1 : 0;
     dim3 grid(wgs, a.tokens);
     switch (a.w.scale_mode * 3 + a.prologue) {
 #define IRIS_PERSISTENT(M, P)                                                                                   \
     case M * 3 + P:                                                                                             \
-        hipLaunchKernelGGL((q8_gemv_persistent<M, W, P>), grid, dim3(W * 64), shmem, stream, a, split, ahead); \
+        hipLaunchKernelGGL((q8_gemv_persistent<M, W, P>), grid, dim3(W * 64), shmem, stream, a, split, ahead, \
+                           wave_stage);                                                                      \
         break;
 #define IRIS_PERSISTENT_M(M) IRIS_PERSISTENT(M, PRO_NONE) IRIS_PERSISTENT(M, PRO_RMSNORM) IRIS_PERSISTENT(M, PRO_NORM_RES_NORM)
         IRIS_PERSISTENT_M(Q8_SCALE_ROW)
