@@ -746,14 +746,15 @@ __global__ __launch_bounds__(W * 64, 4) void q8_gemv_persistent(const GemvArgs a
     const uint32_t part = wave % split;
     const uint32_t slot = part * 4 + g, nslots = split * 4;
 
-    // The first `ahead` batches (one by default, the second then going out
-    // right after the staging) of this wave's first tile go out right after
-    // the row's own loads (the weights do not depend on the row), so the
-    // weight latency runs under the staging. One batch ahead measured faster
-    // than two on every decode product: the fewer weight loads queue in
-    // front of the other waves' row loads on the CU, the sooner those rows
-    // arrive (N=14336, K=4096: 15.71 -> 15.30 us; Gemma-2B decode 1.758 ->
-    // 1.728 ms per token; Mistral-7B 2.705 -> 2.695 ms).
+    // The first `ahead` batches (one or two, the launcher's choice; with one
+    // the second goes out right after the staging) of this wave's first tile
+    // go out right after the row's own loads (the weights do not depend on
+    // the row), so the weight latency runs under the staging. The fewer
+    // weight loads queue in front of the other waves' row loads on the CU,
+    // the sooner those rows arrive: one batch ahead is faster wherever a
+    // workgroup streams less than 192 KB (N=14336, K=4096: 15.71 -> 15.30
+    // us; Gemma-2B decode 1.758 -> 1.728 ms per token), two where it
+    // streams more (Mistral-7B gate/up and head; decode 2.668 -> 2.653 ms).
     // Unconditional, from clamped indices (a wave past the last tile or a
     // lane without blocks reads valid blocks it never uses): a load behind a
     // branch would make the counted waits of the staging wait for it.
@@ -947,7 +948,11 @@ int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) 
     const uint32_t groups = (a.w.tiles + W / split - 1) / (W / split);
     const uint32_t wgs = min(groups, (uint32_t)resident);
     const size_t shmem = (size_t)MAX_LIMBS * a.w.cols;
-    const uint32_t ahead = g_ahead_override ? g_ahead_override : 1;
+    // Two weight batches ahead where an 8-wave workgroup streams at least
+    // 192 KB (Mistral-7B gate/up 28.3 -> 27.7 us, head 30.0 -> 28.7 us), one
+    // elsewhere (two put q/k/v at 13.4 -> 13.9 us and slow the short rows).
+    const uint64_t wg_bytes = (uint64_t)(W / split) * Q8_TILE_ROWS * a.w.cols;
+    const uint32_t ahead = g_ahead_override ? g_ahead_override : (W == 8 && wg_bytes >= (192u << 10) ? 2 : 1);
     // Each wave stages its own blocks' planes when the prologue allows it
     // (no norm, or a norm from the producer's slots).
     const bool eligible = a.prologue == PRO_NONE || (a.prologue == PRO_RMSNORM && a.ssq_in != nullptr);
