@@ -43,7 +43,11 @@ def device():
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
 
 
-@pytest.mark.parametrize("rows,cols,tokens", [(1, 32, 1), (16, 32, 16), (17, 64, 15), (130, 96, 33), (300, 1536, 70)])
+# (200, 4160, 1) and (64, 8224, 1): one-row products whose waves stage their
+# own blocks' planes (8- and 16-wave workgroups, a block count that leaves
+# the last run of four blocks partial).
+@pytest.mark.parametrize("rows,cols,tokens", [(1, 32, 1), (16, 32, 16), (17, 64, 15), (130, 96, 33), (300, 1536, 70),
+                                              (200, 4160, 1), (64, 8224, 1), (48, 4096, 2)])
 @pytest.mark.parametrize("max_exponent,magnitude_bits", [(30, 32), (18, 20), (5, 12)])
 def test_products_equal_one_dot_row_per_value(rows, cols, tokens, max_exponent, magnitude_bits):
     print(f"shape {rows}x{cols} tokens {tokens} regime {max_exponent}/{magnitude_bits}", flush=True)
