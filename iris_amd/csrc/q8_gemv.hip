@@ -887,7 +887,7 @@ constexpr uint32_t WGS_PER_CU = 2;
 int g_num_cus = 0;
 uint32_t g_split_override = 0;
 uint32_t g_ahead_override = 0;  // weight batches issued before the row staging (1 or 2)
-uint32_t g_wave_stage = 1;      // 0: workgroup staging; 1: per-wave where each part has one wave; 2: wherever it applies
+uint32_t g_wave_stage = 1;  // 0: workgroup staging; 1: per wave where each part has one wave (K >= 4096); 2: wherever it applies
 
 void gemv_prepare_once() {
     static bool done = false;
