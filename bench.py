@@ -144,6 +144,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=8)
     ap.add_argument("--cpu-steps", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--direct-launches", action="store_true",
+                    help="time the decodes launch by launch instead of as graph replays (for kernel traces)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X: the library has no multi-GPU path (run with --gpus 1)",
@@ -155,6 +157,7 @@ def main():
 
     from iris_amd import decode_timing, native, synth
 
+    decode_timing.USE_GRAPH = not args.direct_launches
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
     bench = decode_timing.DecodeBench(max(args.steps, args.warmup), log=log)
     if args.warmup:
@@ -235,7 +238,8 @@ def main():
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8xi32->i64 exact",
         "data": "synthetic (random-init Q8_0 weights from a seed, uniform prompt ids)",
         "config": {"workload": "mistral-7b-shape Q8_0 greedy decode, prompt 512 + 512 tokens, batch 1",
-                   "prompt_tokens": PROMPT, "decode_steps_timed": args.steps, "batch": 1},
+                   "prompt_tokens": PROMPT, "decode_steps_timed": args.steps, "batch": 1,
+                   "decode_launches": "direct" if args.direct_launches else "graph replay"},
         "roofline": roof,
         "gemv_per_block": gemv_pb,
         "c2_gemm": c2,

@@ -209,6 +209,16 @@ extern "C" {
         prefill_ms: *mut f64,
         out_tokens: *mut i32,
     ) -> c_int;
+    pub fn iris_session_time_decode_launches(
+        session: *mut IrisSession,
+        prompt: *const i32,
+        prompt_len: u32,
+        steps: u32,
+        use_graph: c_int,
+        ms_per_token: *mut f64,
+        prefill_ms: *mut f64,
+        out_tokens: *mut i32,
+    ) -> c_int;
     pub fn iris_session_time_pass(session: *mut IrisSession, ids: *const i32, count: u32, ms: *mut f64) -> c_int;
     pub fn iris_attention_numerics(
         diff: *const u32,

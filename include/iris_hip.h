@@ -261,6 +261,14 @@ int iris_session_read_kv(IrisSession* session, uint32_t layer, uint32_t pos0, ui
 int iris_session_time_decode(IrisSession* session, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,
                              double* ms_per_token, double* prefill_ms, int32_t* out_tokens);
 
+/* iris_session_time_decode with the decode passes issued as graph replays
+ * (use_graph != 0, the same as iris_session_time_decode) or launch by launch
+ * from the host (use_graph == 0: the same kernels and arguments; what a
+ * kernel tracer sees without graph interception). */
+int iris_session_time_decode_launches(IrisSession* session, const int32_t* prompt, uint32_t prompt_len,
+                                      uint32_t steps, int use_graph, double* ms_per_token, double* prefill_ms,
+                                      int32_t* out_tokens);
+
 /* Times one pass of every layer over `count` rows at position 0 (the
  * teacher-forced pass without downloading rows or hashing) with HIP events
  * on the session's stream. */

@@ -1288,6 +1288,11 @@ int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, d
 
 int iris_session_time_decode(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,
                              double* ms_per_token, double* prefill_ms, int32_t* out_tokens) {
+    return iris_session_time_decode_launches(s, prompt, prompt_len, steps, 1, ms_per_token, prefill_ms, out_tokens);
+}
+
+int iris_session_time_decode_launches(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t steps,
+                                      int use_graph, double* ms_per_token, double* prefill_ms, int32_t* out_tokens) {
     if (!s || !prompt || !ms_per_token || steps == 0) return IRIS_E_INVALID;
     const IrisModelDesc& d = s->model->d;
     if (prompt_len == 0 || prompt_len > s->max_rows) return IRIS_E_RANGE;
@@ -1305,12 +1310,13 @@ int iris_session_time_decode(IrisSession* s, const int32_t* prompt, uint32_t pro
     if (rc == 0) rc = session_head_select(s, prompt_len);
     // Capture (outside the timed region) before timing the replays.
     if (rc == 0) rc = (int)hipEventRecord(e1, s->stream);
-    if (rc == 0) rc = ensure_graph(s, true);
+    if (rc == 0 && use_graph) rc = ensure_graph(s, true);
     float pre = 0.f, dec = 0.f;
     if (rc == 0) rc = (int)hipEventSynchronize(e1);
     if (rc == 0) rc = (int)hipEventElapsedTime(&pre, e0, e1);
     if (rc == 0) rc = (int)hipEventRecord(e1, s->stream);
-    for (uint32_t t = 0; rc == 0 && t < steps; t++) rc = (int)hipGraphLaunch(s->graph_exec, s->stream);
+    for (uint32_t t = 0; rc == 0 && t < steps; t++)
+        rc = use_graph ? (int)hipGraphLaunch(s->graph_exec, s->stream) : session_decode_pass(s, 0);
     if (rc == 0) rc = (int)hipEventRecord(e2, s->stream);
     if (rc == 0) rc = (int)hipEventSynchronize(e2);
     if (rc == 0) rc = (int)hipEventElapsedTime(&dec, e1, e2);

@@ -22,6 +22,10 @@ from . import native, synth
 from .direct import DeviceModel, Session
 
 PROMPT = 512
+# The timed decodes replay the step as a HIP graph (True) or issue its
+# launches one by one (False: the same kernels and time, and what a kernel
+# tracer follows without intercepting graph launches).
+USE_GRAPH = True
 MISTRAL_7B_SEED = 0x7B7B
 PROMPT_SEED = 0x5EED
 # Q8_0 bytes of every product one decode step reads at Mistral-7B shape:
@@ -207,7 +211,7 @@ class DecodeBench:
     def run(self, steps: int):
         """(ms per decode step, prompt-pass ms, token ids) for one timed
         decode of `steps` steps after the prompt pass."""
-        return self.session.time_decode(self.prompt, steps)
+        return self.session.time_decode(self.prompt, steps, use_graph=USE_GRAPH)
 
     def bytes_per_step(self, steps: int) -> float:
         """HBM bytes one decode step must read: every weight once plus the
@@ -263,7 +267,7 @@ class GemmaDecodeBench:
         self.prompt = synth.token_ids(PROMPT_SEED, GEMMA_PROMPT, self.shape.vocab_size)
 
     def run(self, steps: int):
-        return self.session.time_decode(self.prompt, steps)
+        return self.session.time_decode(self.prompt, steps, use_graph=USE_GRAPH)
 
     def bytes_per_step(self, steps: int) -> float:
         """Weights (decode_step_bytes) plus every layer's K and V up to the

@@ -54,6 +54,8 @@ def _declare():
         "iris_session_layer_stage": (C.c_int, [vp, u32, vp, u32, u32, vp, vp]),
         "iris_session_write_kv": (C.c_int, [vp, u32, u32, u32, vp, vp]),
         "iris_session_time_decode": (C.c_int, [vp, vp, u32, u32, C.POINTER(C.c_double), C.POINTER(C.c_double), vp]),
+        "iris_session_time_decode_launches": (C.c_int, [vp, vp, u32, u32, C.c_int, C.POINTER(C.c_double),
+                                                        C.POINTER(C.c_double), vp]),
         "iris_session_time_pass": (C.c_int, [vp, vp, u32, C.POINTER(C.c_double)]),
         "iris_session_read_kv": (C.c_int, [vp, u32, u32, u32, vp, vp]),
         "iris_sha256_bytes": (C.c_int, [vp, u64, vp]),
@@ -244,13 +246,15 @@ class Session:
         native.check(native.lib().iris_session_write_kv(self._h, layer, pos0, k.shape[0], k.ctypes.data,
                                                         v.ctypes.data), "write kv")
 
-    def time_decode(self, prompt_ids, steps: int):
-        """(ms per decode token, prefill ms, generated ids) from HIP events."""
+    def time_decode(self, prompt_ids, steps: int, use_graph: bool = True):
+        """(ms per decode token, prefill ms, generated ids) from HIP events;
+        the decode passes as graph replays, or launch by launch."""
         prompt = np.ascontiguousarray(prompt_ids, dtype=np.int32)
         ms, pre = C.c_double(), C.c_double()
         toks = np.zeros(steps + 1, dtype=np.int32)
-        native.check(native.lib().iris_session_time_decode(self._h, prompt.ctypes.data, prompt.size, steps,
-                                                           C.byref(ms), C.byref(pre), toks.ctypes.data),
+        native.check(native.lib().iris_session_time_decode_launches(self._h, prompt.ctypes.data, prompt.size, steps,
+                                                                    int(use_graph), C.byref(ms), C.byref(pre),
+                                                                    toks.ctypes.data),
                      "time decode")
         return ms.value, pre.value, toks.tolist()
 
