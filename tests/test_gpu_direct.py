@@ -40,6 +40,23 @@ def test_small_mistral_generation_matches_oracle(use_graph):
     assert np.array_equal(got.logits, np.stack(want_logits))
 
 
+@pytest.mark.parametrize("use_graph", [True, False])
+def test_timed_decode_generates_the_oracle_tokens(use_graph):
+    # The benchmark's timed decode (graph replays or launch by launch):
+    # the prompt's selection, then one token per timed step, as the oracle.
+    m = synth.mistral_model(128, 2, 4, 2, 32, 256, 512, seed=23, per_row_scale=True)
+    prompt = synth.token_ids(4, 7, 512)
+    print(f"timed decode, graph={use_graph}", flush=True)
+    dm = DeviceModel(m)
+    s = Session(dm, 64, 16)
+    ms, prefill, tokens = s.time_decode(prompt, 12, use_graph=use_graph)
+    want_tokens, _ = _oracle_generate(m, prompt, 13, 64)
+    # The oracle stops at an end-of-sequence id; the timed decode does not.
+    assert tokens[:len(want_tokens)] == want_tokens
+    assert len(want_tokens) == 13 or want_tokens[-1] in m.eos_token_ids
+    assert ms > 0 and prefill > 0
+
+
 @pytest.mark.parametrize("case", [0, 1, 2])
 def test_parity_mistral_bundle_cases(case):
     g = golden("parity_bundles.json")["bundles"]["parity-mistral"]
