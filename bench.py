@@ -157,6 +157,10 @@ def main():
 
     from iris_amd import decode_timing, native, synth
 
+    if not args.direct_launches and native.kernel_tracer_loaded():
+        # The library refuses graph replays under a kernel tracer.
+        log("kernel tracer loaded: timing the decodes launch by launch")
+        args.direct_launches = True
     decode_timing.USE_GRAPH = not args.direct_launches
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
     bench = decode_timing.DecodeBench(max(args.steps, args.warmup), log=log)

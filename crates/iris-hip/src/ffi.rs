@@ -87,6 +87,7 @@ extern "C" {
         workspace_bytes: u64,
         stream: *mut c_void,
     ) -> c_int;
+    pub fn q8gpu_prepare_matrix_cores(matrix: *mut Q8GpuMatrix, stream: *mut c_void) -> c_int;
     pub fn q8gpu_product_device_noalloc(
         matrix: *const Q8GpuMatrix,
         d_activations: *const i32,
@@ -219,6 +220,7 @@ extern "C" {
         prefill_ms: *mut f64,
         out_tokens: *mut i32,
     ) -> c_int;
+    pub fn iris_kernel_tracer_loaded() -> c_int;
     pub fn iris_session_time_pass(session: *mut IrisSession, ids: *const i32, count: u32, ms: *mut f64) -> c_int;
     pub fn iris_attention_numerics(
         diff: *const u32,

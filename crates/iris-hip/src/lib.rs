@@ -8,17 +8,15 @@
 //!   crates/inference/direct/src/executor.rs:41-290) and the staged
 //!   teacher-forced pass over ranges with carried keys
 //!   (crates/inference/kernels/src/mistral/stage.rs:172-226).
-//! - with the `kernels` feature, [`backend`]: the drop-in for
-//!   inference-kernels' `gpu` module (`slab_product`,
-//!   crates/inference/kernels/src/gpu.rs:233-309) over `MatrixSource`.
+//!
+//! inference-kernels' own `gpu` module (crates/inference/kernels/src/gpu.rs)
+//! needs none of this: it links the five `q8gpu_*` symbols of the library
+//! unchanged.
 //!
 //! Every call returns `Err` with the library's own text for any nonzero
 //! code; nothing falls back to the CPU here.
 
 pub mod ffi;
-
-#[cfg(feature = "kernels")]
-pub mod backend;
 
 use std::ffi::{CStr, CString};
 use std::fmt;
@@ -49,6 +47,7 @@ pub const E_NOMEM: i32 = -3;
 pub const E_STATE: i32 = -4;
 pub const E_RANGE: i32 = -5;
 pub const E_SCRATCH: i32 = -6;
+pub const E_TRACED: i32 = -7;
 
 pub fn error_text(code: i32) -> String {
     // SAFETY: q8gpu_error returns a static NUL-terminated string for any code.
@@ -78,8 +77,9 @@ pub struct DeviceMatrix {
     pub cols: usize,
 }
 
-// SAFETY: the library serialises its host round trip and a matrix is
-// immutable once uploaded; products may be issued from any thread.
+// SAFETY: the library serialises its host round trip, and a matrix changes
+// only through `prepare_matrix_cores`, which takes `&mut self` (no product
+// can run on it meanwhile); products may be issued from any thread.
 unsafe impl Send for DeviceMatrix {}
 unsafe impl Sync for DeviceMatrix {}
 
@@ -136,6 +136,14 @@ impl DeviceMatrix {
             "Q8_0 product",
         )?;
         Ok(out)
+    }
+
+    /// Folds a per-block scale matrix for the int8 matrix cores, so that its
+    /// multi-token products run there (more device memory, see `info`);
+    /// nothing for a row-scale matrix. Synchronous.
+    pub fn prepare_matrix_cores(&mut self) -> Result<()> {
+        // SAFETY: a live matrix, borrowed mutably: no other call uses it.
+        check(unsafe { ffi::q8gpu_prepare_matrix_cores(self.ptr, std::ptr::null_mut()) }, "prepare matrix cores")
     }
 
     /// (rows, cols, scale layout, device bytes).

@@ -9,7 +9,10 @@
  * count or reduction order.
  *
  * Return codes: 0 is success; a positive value is a hipError_t; a negative
- * value is a library code (see q8gpu_error for its text).
+ * value is a library code (see q8gpu_error for its text): -1 invalid
+ * argument or shape, -2 non-finite Q8_0 scale, -3 host allocation failed,
+ * -4 wrong state, -5 past the object's capacity, -6 past the no-allocation
+ * scratch, -7 graph replays asked for under a kernel tracer.
  */
 #ifndef IRIS_HIP_H
 #define IRIS_HIP_H
@@ -74,11 +77,27 @@ uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* matrix, uint32_t tokens);
 
 /* q8gpu_product_device with caller-provided device work space of at least
  * q8gpu_workspace_bytes: a multi-token product of a matrix whose blocks share
- * one scale per row then runs on the int8 matrix cores (same bits). NULL work
- * space = q8gpu_product_device. Returns IRIS_E_RANGE (-5) when it is too
- * small. The synchronous q8gpu_product uses its own work space. */
+ * one scale per row, or of a per-block scale matrix that
+ * q8gpu_prepare_matrix_cores has folded, then runs on the int8 matrix cores
+ * (same bits). NULL work space = q8gpu_product_device. Returns IRIS_E_RANGE
+ * (-5) when it is too small. Asynchronous: it allocates nothing and never
+ * changes the matrix. The synchronous q8gpu_product uses its own work
+ * space. */
 int q8gpu_product_device_ws(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens,
                             int32_t* d_out, void* d_workspace, uint64_t workspace_bytes, void* stream);
+
+/* Folds a per-block scale matrix's scales into weight digit planes so that
+ * its multi-token products (q8gpu_product_device_ws, _noalloc and
+ * q8gpu_product) run on the int8 matrix cores. Allocates up to
+ * Q8_FOLD_MAX_PLANES (4) x rows x cols bytes more device memory (reported by
+ * q8gpu_matrix_info's bytes) and synchronises `stream`. Does nothing, and
+ * returns 0, for a row-scale matrix, one already prepared, or one whose
+ * scales spread over too many binary orders (its products stay on the
+ * vector path, same bits). Not to be called while other calls use the
+ * matrix. No counterpart in the reference (whose device cache budgets
+ * rows*cols + blocks*8 bytes per matrix, gpu.rs:171-173: a prepared matrix
+ * holds more). */
+int q8gpu_prepare_matrix_cores(Q8GpuMatrix* matrix, void* stream);
 
 /* Bytes of each device's scratch array (below): 32 MiB. */
 #define IRIS_NOALLOC_SCRATCH_BYTES (32ull << 20)
@@ -196,7 +215,10 @@ void iris_session_free(IrisSession* session);
  * the budget, else one pass over the selected token's row. out_tokens gets up
  * to `tokens` ids and *out_count how many were produced; out_logits (nullable,
  * tokens x vocab) the logits each selection was made from. use_graph = 1
- * replays each decode pass as a captured HIP graph. */
+ * replays each decode pass as a captured HIP graph; it returns -7, and runs
+ * nothing, while a kernel tracer is loaded in the process (see
+ * iris_kernel_tracer_loaded). A model of no layers is accepted (embedding,
+ * final norm, head, selection). */
 int iris_session_generate(IrisSession* session, const int32_t* prompt, uint32_t prompt_len, uint32_t tokens,
                           const int32_t* eos_ids, uint32_t n_eos, int32_t* out_tokens, uint32_t* out_count,
                           int32_t* out_logits, int32_t use_graph);
@@ -264,10 +286,18 @@ int iris_session_time_decode(IrisSession* session, const int32_t* prompt, uint32
 /* iris_session_time_decode with the decode passes issued as graph replays
  * (use_graph != 0, the same as iris_session_time_decode) or launch by launch
  * from the host (use_graph == 0: the same kernels and arguments; what a
- * kernel tracer sees without graph interception). */
+ * kernel tracer sees without graph interception). Graph replays return -7
+ * while a kernel tracer is loaded. */
 int iris_session_time_decode_launches(IrisSession* session, const int32_t* prompt, uint32_t prompt_len,
                                       uint32_t steps, int use_graph, double* ms_per_token, double* prefill_ms,
                                       int32_t* out_tokens);
+
+/* 1 when a kernel tracer (the ROCm profiler SDK, as rocprofv3 loads it, or
+ * the older rocprofiler) is loaded in this process, else 0. Graph replays of
+ * the decode pass are refused then: under rocprofv3 --kernel-trace they
+ * ended in a segfault inside the HIP runtime with no cause shown in this
+ * library. No counterpart in the reference. */
+int iris_kernel_tracer_loaded(void);
 
 /* Times one pass of every layer over `count` rows at position 0 (the
  * teacher-forced pass without downloading rows or hashing) with HIP events

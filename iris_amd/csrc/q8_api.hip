@@ -171,6 +171,8 @@ const char* q8gpu_error(int code) {
         case IRIS_E_STATE: return "call made in the wrong state";
         case IRIS_E_RANGE: return "position or size past what the object was built for";
         case IRIS_E_SCRATCH: return "work space needed exceeds the no-allocation scratch (IRIS_NOALLOC_SCRATCH_BYTES)";
+        case IRIS_E_TRACED:
+            return "graph replays are not run while a kernel tracer is loaded; decode launch by launch (use_graph = 0)";
         default: break;
     }
     if (code < 0) return g_error_text ? g_error_text : "unknown library error";
@@ -281,11 +283,11 @@ uint64_t q8gpu_workspace_bytes(const Q8GpuMatrix* m, uint32_t tokens) {
 
 }  // extern "C"
 
-// The product with optional work space; `may_fold` lets a per-block scale
-// matrix be folded for the matrix cores (which allocates) on its first
-// multi-token product.
+// The product with optional work space. A per-block scale matrix takes the
+// matrix cores only once q8gpu_prepare_matrix_cores has folded it; nothing
+// here allocates, synchronises or changes the matrix.
 static int product_with_space(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
-                              void* d_workspace, uint64_t workspace_bytes, void* stream, bool may_fold) {
+                              void* d_workspace, uint64_t workspace_bytes, void* stream) {
     if (!m || (tokens && (!d_act || !d_out))) return IRIS_E_INVALID;
     GemvArgs a{};
     a.w = q8_view(m);
@@ -298,11 +300,6 @@ static int product_with_space(const Q8GpuMatrix* m, const int32_t* d_act, uint32
     a.out_stride = m->rows;
     if (d_workspace && tokens >= 2) {
         if (workspace_bytes < q8gpu_workspace_bytes(m, tokens)) return IRIS_E_RANGE;
-        if (may_fold) {
-            const int rc = iris_q8_prepare_fold(const_cast<Q8GpuMatrix*>(m), (hipStream_t)stream);
-            if (rc != 0) return rc;
-            a.w = q8_view(m);
-        }
         a.planes = (int8_t*)d_workspace;
         a.token_limbs = (int32_t*)((char*)d_workspace + planes_bytes(m->cols, tokens));
     }
@@ -313,7 +310,12 @@ extern "C" {
 
 int q8gpu_product_device_ws(const Q8GpuMatrix* m, const int32_t* d_act, uint32_t tokens, int32_t* d_out,
                             void* d_workspace, uint64_t workspace_bytes, void* stream) {
-    return product_with_space(m, d_act, tokens, d_out, d_workspace, workspace_bytes, stream, true);
+    return product_with_space(m, d_act, tokens, d_out, d_workspace, workspace_bytes, stream);
+}
+
+int q8gpu_prepare_matrix_cores(Q8GpuMatrix* m, void* stream) {
+    if (!m) return IRIS_E_INVALID;
+    return iris_q8_prepare_fold(m, (hipStream_t)stream);
 }
 
 // q8gpu_product_device_ws with the device's scratch array as the work space:
@@ -329,7 +331,7 @@ int q8gpu_product_device_noalloc(const Q8GpuMatrix* m, const int32_t* d_act, uin
     uint8_t* ws = nullptr;
     const int rc = scratch_for_current_device(&ws);
     if (rc != 0) return rc;
-    return product_with_space(m, d_act, tokens, d_out, ws, IRIS_NOALLOC_SCRATCH_BYTES, stream, false);
+    return product_with_space(m, d_act, tokens, d_out, ws, IRIS_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int q8gpu_product(const Q8GpuMatrix* m, const int32_t* activations, uint32_t tokens, int32_t* out) {

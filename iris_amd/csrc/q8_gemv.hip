@@ -885,9 +885,6 @@ constexpr uint32_t PERSISTENT_MAX_K = 24576;  // digit planes of a whole row: 5*
 constexpr uint32_t WGS_PER_CU = 2;
 
 int g_num_cus = 0;
-uint32_t g_split_override = 0;
-uint32_t g_ahead_override = 0;  // weight batches issued before the row staging (1 or 2)
-uint32_t g_wave_stage = 1;  // 0: workgroup staging; 1: per wave where each part has one wave (K >= 4096); 2: wherever it applies
 
 void gemv_prepare_once() {
     static bool done = false;
@@ -907,9 +904,6 @@ void gemv_prepare_once() {
         hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
 #undef IRIS_PERSISTENT_P
 #undef IRIS_PERSISTENT_W
-    if (const char* e = getenv("IRIS_GEMV_SPLIT")) g_split_override = (uint32_t)atoi(e);
-    if (const char* e = getenv("IRIS_GEMV_AHEAD")) g_ahead_override = (uint32_t)atoi(e) == 1 ? 1 : 2;
-    if (const char* e = getenv("IRIS_GEMV_WAVE_STAGE")) g_wave_stage = (uint32_t)atoi(e) > 2 ? 2 : (uint32_t)atoi(e);
 }
 
 // Waves sharing one tile (of a workgroup's W): the most that still give a
@@ -920,9 +914,6 @@ void gemv_prepare_once() {
 // idle (N=14336, K=4096: split 4 at 448 of 512 groups is 10% faster than
 // split 8 at 1.75 rounds); one wave per tile is slower at every size.
 uint32_t choose_split(uint32_t tiles, uint32_t w, uint64_t wgs) {
-    if (g_split_override == 1 || g_split_override == 2 || g_split_override == 4 || g_split_override == 8 ||
-        (g_split_override == 16 && w == 16))
-        return g_split_override;
     uint32_t best = 0;
     for (uint32_t s = 2; s <= w; s *= 2)
         if ((uint64_t)tiles * s / w <= wgs) best = s;
@@ -952,15 +943,14 @@ int launch_persistent(const GemvArgs& a, hipStream_t stream, uint64_t resident) 
     // 192 KB (Mistral-7B gate/up 28.3 -> 27.7 us, head 30.0 -> 28.7 us), one
     // elsewhere (two put q/k/v at 13.4 -> 13.9 us and slow the short rows).
     const uint64_t wg_bytes = (uint64_t)(W / split) * Q8_TILE_ROWS * a.w.cols;
-    const uint32_t ahead = g_ahead_override ? g_ahead_override : (W == 8 && wg_bytes >= (192u << 10) ? 2 : 1);
+    const uint32_t ahead = W == 8 && wg_bytes >= (192u << 10) ? 2 : 1;
     // Each wave stages its own blocks' planes when the prologue allows it
     // (no norm, or a norm from the producer's slots).
     const bool eligible = a.prologue == PRO_NONE || (a.prologue == PRO_RMSNORM && a.ssq_in != nullptr);
     // Per wave where every split part has one wave and rows are at least
     // 4096 long (K=2048, Gemma-2B's O: 7.8 -> 8.3 us per wave; K=4096 and
     // K=14336, 16384: faster).
-    const uint32_t wave_stage =
-        eligible && (g_wave_stage == 2 || (g_wave_stage == 1 && split == W && a.w.cols >= 4096)) ? 1 : 0;
+    const uint32_t wave_stage = eligible && split == W && a.w.cols >= 4096 ? 1 : 0;
     dim3 grid(wgs, a.tokens);
     switch (a.w.scale_mode * 3 + a.prologue) {
 #define IRIS_PERSISTENT(M, P)                                                                                   \

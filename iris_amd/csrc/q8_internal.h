@@ -14,6 +14,7 @@ enum {
     IRIS_E_STATE = -4,        // call made in the wrong state (e.g. before finalize)
     IRIS_E_RANGE = -5,        // position or size past what the object was built for
     IRIS_E_SCRATCH = -6,      // work space needed exceeds the no-allocation scratch
+    IRIS_E_TRACED = -7,       // graph replays asked for while a kernel tracer is loaded
 };
 
 // Scale layouts of a device Q8_0 matrix.

@@ -14,6 +14,8 @@
 // kernel selects the first maximum and embeds the next row. Positions and
 // the step counter live in device memory, so a decode pass is the same
 // launch sequence every time and is captured once as a HIP graph.
+#include <link.h>
+
 #include <algorithm>
 #include <atomic>
 #include <cstdlib>
@@ -49,12 +51,20 @@ int layer_of(const std::string& name, std::string* suffix) {
         if (rc_ != 0) return rc_;       \
     } while (0)
 
-// False when a block of raw Q8_0 rows has a non-finite f16 scale (exponent
-// 0x1f), which dequantize_row refuses (q8.rs:45-47, 76-92).
-bool q8_scales_finite(const uint8_t* raw, size_t blocks) {
-    for (size_t b = 0; b < blocks; b++)
-        if ((raw[b * 34 + 1] & 0x7c) == 0x7c) return false;
-    return true;
+// The rows of a Q8_0 table (rows of row_bytes) holding a block with a
+// non-finite f16 scale (exponent 0x1f), which dequantize_row refuses
+// (q8.rs:45-47, 76-92): one flag per row, or none at all when every scale
+// is finite.
+std::vector<uint8_t> q8_rows_refused(const uint8_t* raw, size_t rows, size_t row_bytes) {
+    std::vector<uint8_t> bad;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t b = 0; b < row_bytes / 34; b++)
+            if ((raw[r * row_bytes + b * 34 + 1] & 0x7c) == 0x7c) {
+                if (bad.empty()) bad.assign(rows, 0);
+                bad[r] = 1;
+                break;
+            }
+    return bad;
 }
 
 template <class T>
@@ -128,10 +138,16 @@ int iris_model_create(const IrisModelDesc* desc, IrisModel** out) {
     const IrisModelDesc& d = *desc;
     const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
     if (d.family != IRIS_FAMILY_MISTRAL_DENSE && !gemma) return IRIS_E_INVALID;
-    if (!d.hidden || !d.layers || !d.heads || !d.kv_heads || !d.head_dim || !d.ffn || !d.vocab) return IRIS_E_INVALID;
-    if (d.heads % d.kv_heads || d.head_dim % 4 || d.hidden % 32 || d.norm_eps < 0) return IRIS_E_INVALID;
-    if (d.head_dim > ATTN_MAX_HEAD_DIM) return IRIS_E_INVALID;
-    if (gemma) {
+    if (!d.hidden || !d.vocab || d.hidden % 32 || d.norm_eps < 0) return IRIS_E_INVALID;
+    // A model of no layers is embedding, final norm, head and selection
+    // (executor.rs:293-360 over an empty layer list; build_ple_params,
+    // model.rs:679-686, makes no PLE inputs): the attention, FFN and PLE
+    // shape fields are not read.
+    if (d.layers) {
+        if (!d.heads || !d.kv_heads || !d.head_dim || !d.ffn) return IRIS_E_INVALID;
+        if (d.heads % d.kv_heads || d.head_dim % 4 || d.head_dim > ATTN_MAX_HEAD_DIM) return IRIS_E_INVALID;
+    }
+    if (gemma && d.layers) {
         const uint32_t ghd = d.global_head_dim ? d.global_head_dim : d.head_dim;
         // The PLE segments are whole Q8_0 blocks of embed_tokens_per_layer.
         if (ghd % 4 || ghd > ATTN_MAX_HEAD_DIM || !d.ple_width || d.ple_width % 32 || d.ple_width > GEMMA_MAX_PLE)
@@ -228,7 +244,11 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
     }
     if (name == std::string(PREFIX) + "embed_tokens.weight") {
         if (width != 8 || rows != d.vocab || cols != d.hidden) return IRIS_E_INVALID;
-        if (!q8_scales_finite((const uint8_t*)data, bytes / 34)) return IRIS_E_SCALE;
+        // A row with a non-finite scale is refused when its token is
+        // embedded (model.rs:316-330), as the reference's lazy dequantize
+        // does; a tied head reads every row for every logit, so there the
+        // upload refuses it.
+        m->embed_bad = q8_rows_refused((const uint8_t*)data, rows, cols / 32 * 34);
         RT_CHECK(dev_alloc_copy(&m->embed_raw, data, bytes));
         m->embed_row_bytes = (uint32_t)(cols / 32 * 34);
         if (d.tied_head) {
@@ -255,7 +275,7 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
         const uint64_t lp = (uint64_t)d.layers * d.ple_width;
         if (name == std::string(PREFIX) + "embed_tokens_per_layer.weight") {
             if (width != 8 || rows != d.vocab || cols != lp) return IRIS_E_INVALID;
-            if (!q8_scales_finite((const uint8_t*)data, bytes / 34)) return IRIS_E_SCALE;
+            m->ple_bad = q8_rows_refused((const uint8_t*)data, rows, cols / 32 * 34);
             RT_CHECK(dev_alloc_copy(&m->embed_ple, data, bytes));
             m->embed_ple_row_bytes = (uint32_t)(cols / 32 * 34);
             return 0;
@@ -288,6 +308,7 @@ int iris_model_set_tensor(IrisModel* m, const char* cname, int32_t width, const 
 // frequency ladders (validated as prefill_range.rs:394-466 does).
 static int gemma_finalize(IrisModel* m) {
     const IrisModelDesc& d = m->d;
+    if (d.layers == 0) return 0;
     if (!m->embed_ple || !m->ple_model_proj || !m->ple_proj_norm) return IRIS_E_STATE;
     const uint32_t rot_full = (uint32_t)(((uint64_t)d.global_head_dim * (uint32_t)d.partial_rotary_q16) >> 16);
     struct Kind {
@@ -337,7 +358,7 @@ int iris_model_finalize(IrisModel* m) {
     if (!m) return IRIS_E_INVALID;
     const IrisModelDesc& d = m->d;
     const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
-    if (!m->embed_raw || !m->head || !m->final_norm || (!gemma && !m->inv_freq)) return IRIS_E_STATE;
+    if (!m->embed_raw || !m->head || !m->final_norm || (!gemma && d.layers && !m->inv_freq)) return IRIS_E_STATE;
     if (gemma) RT_CHECK(gemma_finalize(m));
     for (uint32_t l = 0; l < d.layers; l++) {
         LayerWeights& L = m->layers[l];
@@ -532,7 +553,7 @@ static int mistral_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     const IrisModelDesc& d = m->d;
     // The rows' RoPE (sin, cos) pairs, shared by every layer (for a one-row
     // pass after a selection, the selection kernel has formed them).
-    if (!(rows == 1 && s->rope_ready))
+    if (!(rows == 1 && s->rope_ready) && d.layers)
         RT_CHECK(iris_rope_table_launch(m->inv_freq, d.head_dim / 2, s->d_pos, rows, s->rope_sc, s->stream));
     s->rope_ready = false;
     // One row: sums of squares pass from each residual product to the norm
@@ -785,7 +806,7 @@ static bool gemma_carries(const IrisSession* s, uint32_t rows, const CkptSink* s
 static int gemma_pass(IrisSession* s, uint32_t rows, const CkptSink* sink) {
     const bool carry = gemma_carries(s, rows, sink);
     s->carry = IrisSession::GemmaCarry{};
-    RT_CHECK(gemma_ple(s, rows));
+    if (s->model->d.layers) RT_CHECK(gemma_ple(s, rows));
     for (uint32_t l = 0; l < s->model->d.layers; l++) {
         RT_CHECK(gemma_layer(s, l, rows, carry));
         RT_CHECK(checkpoint_layer(s, sink, l, rows));
@@ -842,7 +863,7 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     g.x_next = s->x;
     g.ids_next = m->d.family == IRIS_FAMILY_GEMMA_DENSE ? s->ids : nullptr;
     g.sel_partial = s->sel_partial;
-    const bool rope = m->d.family != IRIS_FAMILY_GEMMA_DENSE;
+    const bool rope = m->d.family != IRIS_FAMILY_GEMMA_DENSE && d.layers;
     if (rope) {
         g.rope_next = s->rope_sc;
         g.rope_half = d.head_dim / 2;
@@ -854,13 +875,23 @@ static int session_head_select(IrisSession* s, uint32_t rows) {
     return 0;
 }
 
+// True when embedding token `id` is refused: its embedding row, or for a
+// gemma-dense model with layers its PLE row, has a non-finite block scale
+// (dequantize_row, q8.rs:76-92, when model.rs:316-330 or the PLE prepare
+// reads the row).
+static bool embedding_refused(const IrisModel* m, int32_t id) {
+    return (!m->embed_bad.empty() && m->embed_bad[id]) || (!m->ple_bad.empty() && m->ple_bad[id]);
+}
+
 // The pass's rows: the embedding of `ids` at positions start.., the step
 // counter reset.
 static int session_reset_and_embed(IrisSession* s, const int32_t* ids, uint32_t count, uint32_t start = 0) {
     IrisModel* m = s->model;
     s->rope_ready = false;
-    for (uint32_t i = 0; i < count; i++)
+    for (uint32_t i = 0; i < count; i++) {
         if (ids[i] < 0 || (uint32_t)ids[i] >= m->d.vocab) return IRIS_E_INVALID;
+        if (embedding_refused(m, ids[i])) return IRIS_E_SCALE;
+    }
     RT_CHECK(iris_set_counters_launch(s->d_pos, (int32_t)start, s->d_step, 0, s->stream));
     RT_CHECK(hipMemcpyAsync(s->ids, ids, (size_t)count * 4, hipMemcpyHostToDevice, s->stream));
     return iris_embed_rows_launch(s->ids, count, m->embed_raw, m->embed_row_bytes, m->d.hidden, m->embed_scale, s->x,
@@ -911,10 +942,55 @@ static void cover_all(IrisSession* s, uint32_t pos0, uint32_t count, bool fresh)
     }
 }
 
+// A pass is about to write positions [pos0, pos0 + count) of a layer's
+// cache: until it has succeeded they hold no keys, so the coverage keeps
+// only what lies before them (or after, when nothing lies before). A pass
+// that fails partway then leaves no claim on positions it may have
+// overwritten; a pass that succeeds covers them again.
+static void uncover(IrisSession* s, uint32_t l, uint32_t pos0, uint32_t count) {
+    uint32_t& lo = s->kv_lo[l];
+    uint32_t& hi = s->kv_hi[l];
+    const uint32_t end = pos0 + count;
+    if (lo == hi || end <= lo || pos0 >= hi) return;
+    if (lo < pos0) hi = pos0;
+    else if (end < hi) lo = end;
+    else lo = hi = 0;
+}
+
+static void uncover_all(IrisSession* s, uint32_t pos0, uint32_t count, bool fresh) {
+    for (uint32_t l = 0; l < s->model->d.layers; l++) {
+        if (fresh) s->kv_lo[l] = s->kv_hi[l] = 0;
+        uncover(s, l, pos0, count);
+    }
+}
+
+// True when a kernel tracer is loaded in this process: the ROCm profiler
+// SDK (rocprofv3 preloads its tool, which loads the SDK) or the older
+// rocprofiler. Graph replays of the decode pass ended twice in a segfault
+// inside the HIP runtime under rocprofv3 --kernel-trace with no cause shown
+// on the library's side, so they are refused while a tracer is present;
+// the same pass launched kernel by kernel traces normally.
+static bool kernel_tracer_loaded() {
+    int found = 0;
+    dl_iterate_phdr(
+        [](struct dl_phdr_info* info, size_t, void* data) -> int {
+            const char* n = info->dlpi_name;
+            if (n && (std::strstr(n, "librocprofiler-sdk.so") || std::strstr(n, "librocprofiler-sdk-tool") ||
+                      std::strstr(n, "librocprofiler64"))) {
+                *(int*)data = 1;
+                return 1;
+            }
+            return 0;
+        },
+        &found);
+    return found != 0;
+}
+
 // Captures the decode pass (one row, head, select) as a graph. Each
 // generation captures its own (a few hundred nodes, outside any timed
 // region), so no graph outlives the call that made it.
 static int ensure_graph(IrisSession* s, bool fresh) {
+    if (kernel_tracer_loaded()) return IRIS_E_TRACED;
     if (!fresh && s->graph_exec && s->graph_keep_logits == s->keep_logits) return 0;
     if (s->graph_exec) {
         hipGraphExecDestroy(s->graph_exec);
@@ -1053,15 +1129,16 @@ void iris_session_free(IrisSession* s) {
     delete s;
 }
 
-int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t tokens,
-                          const int32_t* eos_ids, uint32_t n_eos, int32_t* out_tokens, uint32_t* out_count,
-                          int32_t* out_logits, int32_t use_graph) {
+static int session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t tokens,
+                            const int32_t* eos_ids, uint32_t n_eos, int32_t* out_tokens, uint32_t* out_count,
+                            int32_t* out_logits, int32_t use_graph) {
     if (!s || !prompt || !out_tokens || !out_count) return IRIS_E_INVALID;
     *out_count = 0;
     if (prompt_len == 0 || tokens == 0) return tokens == 0 ? 0 : IRIS_E_INVALID;
     IrisModel* m = s->model;
     const IrisModelDesc& d = m->d;
     if (prompt_len > s->max_rows) return IRIS_E_RANGE;
+    if (use_graph && tokens > 1 && kernel_tracer_loaded()) return IRIS_E_TRACED;
     // The last pass runs at position prompt_len + tokens - 2.
     const uint64_t end = (uint64_t)prompt_len + tokens - 1;
     if (end > s->max_positions || end > d.max_positions) return IRIS_E_RANGE;
@@ -1076,9 +1153,10 @@ int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt
             s->logits_keep_cap = need;
         }
     }
+    // The passes fill positions 0..prompt_len + tokens - 1 of every cache
+    // (covered once they have run).
+    uncover_all(s, 0, (uint32_t)end, true);
     RT_CHECK(session_reset_and_embed(s, prompt, prompt_len));
-    // The passes fill positions 0..prompt_len + tokens - 1 of every cache.
-    cover_all(s, 0, (uint32_t)end, true);
     RT_CHECK(session_pass(s, prompt_len, nullptr));
     RT_CHECK(session_head_select(s, prompt_len));
     if (use_graph && tokens > 1) RT_CHECK(ensure_graph(s, true));
@@ -1099,8 +1177,20 @@ int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt
             break;
         }
     }
+    // Each selection but the last is embedded for the next pass
+    // (executor.rs:157-183): a refused row fails the run there.
+    for (uint32_t t = 0; t + 1 < count; t++)
+        if (embedding_refused(m, out_tokens[t])) return IRIS_E_SCALE;
     *out_count = count;
+    cover_all(s, 0, (uint32_t)end, true);
     return 0;
+}
+
+extern "C" int iris_session_generate(IrisSession* s, const int32_t* prompt, uint32_t prompt_len, uint32_t tokens,
+                                     const int32_t* eos_ids, uint32_t n_eos, int32_t* out_tokens,
+                                     uint32_t* out_count, int32_t* out_logits, int32_t use_graph) {
+    return session_generate(s, prompt, prompt_len, tokens, eos_ids, n_eos, out_tokens, out_count, out_logits,
+                            use_graph);
 }
 
 // Staging for the per-layer checkpoints of passes of up to max_rows rows:
@@ -1117,6 +1207,9 @@ static int ensure_checkpoint_space(IrisSession* s) {
     return 0;
 }
 
+static int layer_range_run(IrisSession* s, const int32_t* ids, uint32_t count, uint32_t start_position,
+                           int32_t* out_rows, uint8_t* out_hashes);
+
 // The pass runs on the session's stream, copying each layer's rows aside on
 // the device as it finishes; a second stream brings them to pinned host
 // memory behind it, and host threads hash (and copy out) each layer as it
@@ -1129,7 +1222,17 @@ int iris_session_layer_range(IrisSession* s, const int32_t* ids, uint32_t count,
     const uint64_t end = (uint64_t)start_position + count;
     if (count > s->max_rows || end > d.max_positions || end > s->max_positions) return IRIS_E_RANGE;
     if (!range_covered(s, start_position)) return IRIS_E_STATE;
-    cover_all(s, start_position, count, start_position == 0);
+    // A range at position 0 starts the caches afresh.
+    uncover_all(s, start_position, count, start_position == 0);
+    const int rc = layer_range_run(s, ids, count, start_position, out_rows, out_hashes);
+    if (rc == 0) cover_all(s, start_position, count, false);
+    return rc;
+}
+
+static int layer_range_run(IrisSession* s, const int32_t* ids, uint32_t count, uint32_t start_position,
+                           int32_t* out_rows, uint8_t* out_hashes) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
     if (!out_rows && !out_hashes) {
         RT_CHECK(session_reset_and_embed(s, ids, count, start_position));
         RT_CHECK(session_pass(s, count, nullptr));
@@ -1176,6 +1279,9 @@ int iris_session_layer_pass(IrisSession* s, const int32_t* ids, uint32_t count, 
     return iris_session_layer_range(s, ids, count, 0, out_rows, out_hashes);
 }
 
+static int layer_stage_run(IrisSession* s, uint32_t layer, const int32_t* in_rows, uint32_t count,
+                           uint32_t start_position, const int32_t* ple_rows, int32_t* out_rows);
+
 // One layer over one range (run_layer_stage, mistral/stage.rs:172-226;
 // run_prefill_range_direct, prefill_range.rs:82-172): the layer's input rows
 // come from the host, its output rows go back, and its own keys and values
@@ -1192,7 +1298,22 @@ int iris_session_layer_stage(IrisSession* s, uint32_t layer, const int32_t* in_r
     const LayerWeights& L = m->layers[layer];
     const uint32_t src = (uint32_t)L.kv_source, from = range_needs_from(L, start_position);
     if (from < start_position && (s->kv_lo[src] > from || s->kv_hi[src] < start_position)) return IRIS_E_STATE;
-    cover(s, layer, start_position, count);
+    // A KV-shared gemma layer attends over its donor's cache, which must also
+    // hold the range's own positions: the donor's stage for this range runs
+    // first (model.rs:824-877 donors are earlier layers).
+    if (src != layer && (s->kv_lo[src] == s->kv_hi[src] || s->kv_lo[src] > from || s->kv_hi[src] < end))
+        return IRIS_E_STATE;
+    uncover(s, layer, start_position, count);
+    const int rc = layer_stage_run(s, layer, in_rows, count, start_position, ple_rows, out_rows);
+    if (rc == 0) cover(s, layer, start_position, count);
+    return rc;
+}
+
+static int layer_stage_run(IrisSession* s, uint32_t layer, const int32_t* in_rows, uint32_t count,
+                           uint32_t start_position, const int32_t* ple_rows, int32_t* out_rows) {
+    IrisModel* m = s->model;
+    const IrisModelDesc& d = m->d;
+    const bool gemma = d.family == IRIS_FAMILY_GEMMA_DENSE;
     s->rope_ready = false;
     s->ssq_x_valid = false;
     hipStream_t st = s->stream;
@@ -1266,13 +1387,15 @@ int iris_session_read_kv(IrisSession* s, uint32_t layer, uint32_t pos0, uint32_t
     return 0;
 }
 
+int iris_kernel_tracer_loaded(void) { return kernel_tracer_loaded() ? 1 : 0; }
+
 int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, double* ms) {
     if (!s || !ids || !ms || count == 0) return IRIS_E_INVALID;
     if (count > s->max_rows || count > s->model->d.max_positions) return IRIS_E_RANGE;
     hipEvent_t e0 = nullptr, e1 = nullptr;
     RT_CHECK(hipEventCreate(&e0));
     RT_CHECK(hipEventCreate(&e1));
-    cover_all(s, 0, count, true);
+    uncover_all(s, 0, count, true);
     int rc = session_reset_and_embed(s, ids, count);
     if (rc == 0) rc = (int)hipEventRecord(e0, s->stream);
     if (rc == 0) rc = session_pass(s, count, nullptr);
@@ -1282,7 +1405,10 @@ int iris_session_time_pass(IrisSession* s, const int32_t* ids, uint32_t count, d
     if (rc == 0) rc = (int)hipEventElapsedTime(&t, e0, e1);
     hipEventDestroy(e0);
     hipEventDestroy(e1);
-    if (rc == 0) *ms = t;
+    if (rc == 0) {
+        *ms = t;
+        cover_all(s, 0, count, true);
+    }
     return rc;
 }
 
@@ -1298,12 +1424,13 @@ int iris_session_time_decode_launches(IrisSession* s, const int32_t* prompt, uin
     if (prompt_len == 0 || prompt_len > s->max_rows) return IRIS_E_RANGE;
     const uint64_t end = (uint64_t)prompt_len + steps;
     if (end > s->max_positions || end > d.max_positions) return IRIS_E_RANGE;
+    if (use_graph && kernel_tracer_loaded()) return IRIS_E_TRACED;
     s->keep_logits = false;
     hipEvent_t e0 = nullptr, e1 = nullptr, e2 = nullptr;
     RT_CHECK(hipEventCreate(&e0));
     RT_CHECK(hipEventCreate(&e1));
     RT_CHECK(hipEventCreate(&e2));
-    cover_all(s, 0, (uint32_t)end, true);
+    uncover_all(s, 0, (uint32_t)end, true);
     int rc = session_reset_and_embed(s, prompt, prompt_len);
     if (rc == 0) rc = (int)hipEventRecord(e0, s->stream);
     if (rc == 0) rc = session_pass(s, prompt_len, nullptr);
@@ -1322,12 +1449,20 @@ int iris_session_time_decode_launches(IrisSession* s, const int32_t* prompt, uin
     if (rc == 0) rc = (int)hipEventElapsedTime(&dec, e1, e2);
     if (rc == 0 && out_tokens)
         rc = (int)hipMemcpy(out_tokens, s->tokens, (size_t)(steps + 1) * 4, hipMemcpyDeviceToHost);
+    if (rc == 0 && (!s->model->embed_bad.empty() || !s->model->ple_bad.empty())) {
+        // The selections the timed passes embedded (all but the last).
+        std::vector<int32_t> ids(steps + 1);
+        rc = (int)hipMemcpy(ids.data(), s->tokens, (size_t)(steps + 1) * 4, hipMemcpyDeviceToHost);
+        for (uint32_t t = 0; rc == 0 && t < steps; t++)
+            if (embedding_refused(s->model, ids[t])) rc = IRIS_E_SCALE;
+    }
     hipEventDestroy(e0);
     hipEventDestroy(e1);
     hipEventDestroy(e2);
     if (rc == 0) {
         *ms_per_token = dec / steps;
         if (prefill_ms) *prefill_ms = pre;
+        cover_all(s, 0, (uint32_t)end, true);
     }
     return rc;
 }

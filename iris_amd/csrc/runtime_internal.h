@@ -44,6 +44,10 @@ struct IrisModel {
     std::vector<std::map<std::string, HostTensor>> pending;
     uint8_t* embed_raw = nullptr;   // reference layout, for row lookups
     uint32_t embed_row_bytes = 0;
+    // Per token id, 1 = the embedding row (embed_bad) or the PLE row
+    // (ple_bad) has a non-finite block scale, refused when the token is
+    // embedded; empty when every row's scales are finite.
+    std::vector<uint8_t> embed_bad, ple_bad;
     Q8GpuMatrix* head = nullptr;
     int32_t* final_norm = nullptr;
     int64_t* inv_freq = nullptr;

@@ -89,6 +89,7 @@ def time_host_product(tokens: int, n: int = GEMV_N, k: int = GEMV_K, iterations:
 
     raw = synth.q8_matrix(synth.tensor_seed(2, 1), n, k, synth.scale_base_for(k), True)
     m = Q8Matrix.from_bytes(raw, n, k)
+    m.prepare_matrix_cores()  # a per-block scale matrix is folded for the matrix cores
     if x is None:
         rng = np.random.default_rng(2)
         x = (rng.integers(-127, 128, (tokens, k)) * (256 + int(rng.integers(0, 256)))).astype(np.int32)
@@ -140,6 +141,7 @@ def time_gemm(tokens: int = 2048, n: int = 14336 * 2, k: int = GEMV_K, iteration
 
     raw = synth.q8_matrix(synth.tensor_seed(3, 1), n, k, synth.scale_base_for(k), per_row_scale)
     m = Q8Matrix.from_bytes(raw, n, k)
+    m.prepare_matrix_cores()  # a per-block scale matrix is folded for the matrix cores
     if x is None:
         rng = np.random.default_rng(4)
         half = 1 << (magnitude_bits - 1)
@@ -296,13 +298,14 @@ def time_teacher_forced(rows: int = 2048, repeats: int = 2, log=None, per_row_sc
 
 def trace_decode(steps: int = 64) -> dict:
     """A short decode for kernel traces: a session of 1024 positions, a
-    512-token prompt (ids from seed 1), `steps` greedy steps replayed as a
-    HIP graph, timed with HIP events; nothing else runs."""
+    512-token prompt (ids from seed 1), `steps` greedy steps (graph replays,
+    or launch by launch under a kernel tracer), timed with HIP events;
+    nothing else runs."""
     model = synth.mistral_7b(seed=MISTRAL_7B_SEED)
     dm = DeviceModel(model)
     del model.tensors
     session = Session(dm, 1024, PROMPT)
-    ms, prefill, _ = session.time_decode(synth.token_ids(1, PROMPT, 32000), steps)
+    ms, prefill, _ = session.time_decode(synth.token_ids(1, PROMPT, 32000), steps, use_graph=USE_GRAPH)
     session.free()
     dm.free()
     return {"decode_ms_per_step": round(ms, 4), "prompt_pass_ms": round(prefill, 2), "steps": steps}
@@ -357,6 +360,11 @@ def main(argv=None):
                          "counters); Mistral-7B shape, or Gemma-2B shape with --gemma")
     ap.add_argument("--gemma", action="store_true", help="with --eager-decode: the Gemma-2B shape")
     args = ap.parse_args(argv)
+    global USE_GRAPH
+    if USE_GRAPH and native.kernel_tracer_loaded():
+        # The library refuses graph replays under a kernel tracer.
+        print("kernel tracer loaded: decodes launched one by one", file=sys.stderr, flush=True)
+        USE_GRAPH = False
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
     if args.eager_decode:
         print(json.dumps(eager_decode(args.eager_decode, args.gemma)), flush=True)

@@ -82,7 +82,7 @@ def _desc(model: Model) -> ModelDesc:
         d.attention_scale_q32 = s.attention_scale_q32
         d.max_positions = s.max_positions
     else:
-        d.ffn = model.ffn_size(0)
+        d.ffn = model.ffn_size(0) if model.num_layers else 0
         d.global_head_dim = s.global_head_dim
         d.ple_width = s.hidden_size_per_layer_input
         d.sliding_window = s.sliding_window
@@ -173,6 +173,16 @@ class DeviceModel:
 class GenerateResult:
     token_ids: list
     logits: np.ndarray | None  # [selections, vocab]
+    # "eos" when the last selection is an EOS id, else "max_new_tokens"
+    # (the reference's report field, crates/inference/direct/src/executor.rs:157-171)
+    stop_reason: str = "max_new_tokens"
+
+    @property
+    def token_ids_sha256(self) -> str:
+        """SHA-256 of the ids as compact JSON (``[2,0]``): the reference's
+        generated_token_ids_sha256 (serde_json::to_vec of the id list)."""
+        import hashlib
+        return hashlib.sha256(("[" + ",".join(str(t) for t in self.token_ids) + "]").encode()).hexdigest()
 
 
 class Session:
@@ -197,7 +207,9 @@ class Session:
             out.ctypes.data, C.byref(count), logits.ctypes.data if keep_logits else None, int(use_graph)),
             "generate")
         n = count.value
-        return GenerateResult(out[:n].tolist(), logits[:n] if keep_logits else None)
+        ids = out[:n].tolist()
+        eos = n > 0 and ids[-1] in self.dm.model.eos_token_ids
+        return GenerateResult(ids, logits[:n] if keep_logits else None, "eos" if eos else "max_new_tokens")
 
     def layer_pass(self, ids, keep_rows: bool = True):
         """Teacher-forced pass: (rows [layers, n, hidden] or None, SHA-256 per layer)."""

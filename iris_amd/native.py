@@ -63,6 +63,7 @@ def _declare(L):
         "q8gpu_workspace_bytes": (u64, [vp, u32]),
         "q8gpu_product_device_ws": (C.c_int, [vp, vp, u32, vp, vp, u64, vp]),
         "q8gpu_product_device_noalloc": (C.c_int, [vp, vp, u32, vp, vp]),
+        "q8gpu_prepare_matrix_cores": (C.c_int, [vp, vp]),
         "q8gpu_matrix_info": (C.c_int, [vp, C.POINTER(u32), C.POINTER(u32), C.POINTER(C.c_int), C.POINTER(u64)]),
         "q8gpu_synchronize": (C.c_int, []),
         "iris_device_malloc": (C.c_int, [u64, pp]),
@@ -75,11 +76,18 @@ def _declare(L):
         "iris_silu_device": (C.c_int, [vp, u32, vp]),
         "iris_silu_table_device": (C.c_int, [vp, u32, vp]),
         "iris_time_product_ws": (C.c_int, [vp, vp, u32, vp, vp, u64, u32, C.POINTER(C.c_double)]),
+        "iris_kernel_tracer_loaded": (C.c_int, []),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
         f.restype = res
         f.argtypes = args
+
+
+def kernel_tracer_loaded() -> bool:
+    """True when a kernel tracer (rocprofv3's profiler SDK) is loaded in this
+    process: the library then refuses graph replays of the decode pass."""
+    return bool(lib().iris_kernel_tracer_loaded())
 
 
 def header_functions() -> list:

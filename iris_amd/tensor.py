@@ -52,6 +52,12 @@ class Q8Matrix:
     def handle(self):
         return self._h
 
+    def prepare_matrix_cores(self):
+        """Fold a per-block scale matrix for the int8 matrix cores (more
+        device memory; nothing for a row-scale matrix or a too-wide spread):
+        its multi-token products then run there."""
+        native.check(native.lib().q8gpu_prepare_matrix_cores(self._h, None), "prepare matrix cores")
+
     def info(self):
         r, c, mode, b = C.c_uint32(), C.c_uint32(), C.c_int(), C.c_uint64()
         native.check(native.lib().q8gpu_matrix_info(self._h, C.byref(r), C.byref(c), C.byref(mode), C.byref(b)),
@@ -73,36 +79,49 @@ class Q8Matrix:
 class UploadCache:
     """Device copies of Q8_0 matrices by the key that names their bytes (the
     reference's Q8Key, crates/inference/kernels/src/tensor.rs:90-108: a
-    mapped tensor's (mapping, offset), or a unique key), evicting the least
-    recently used once the held bytes pass ``budget`` (the reference's
-    device cache, crates/inference/kernels/src/gpu.rs:176-208)."""
+    mapped tensor's (mapping, offset), or a unique key), least recently used
+    first out once the held bytes would pass ``budget`` (the reference's
+    device cache, crates/inference/kernels/src/gpu.rs:176-208).
+
+    As there, each entry counts rows * cols + blocks * 8 bytes, fixed when it
+    is inserted (gpu.rs:171-173), and the entries to evict go before the
+    upload. An evicted matrix leaves the cache; its device memory is released
+    when the last holder of the returned Q8Matrix lets it go, so a matrix a
+    caller still holds stays valid."""
 
     def __init__(self, budget: int = 64 << 30):
         from collections import OrderedDict
         self.budget = budget
         self.held = 0
-        self._items = OrderedDict()
+        self._items = OrderedDict()  # key -> (matrix, counted bytes)
         self.uploads = 0
 
+    @staticmethod
+    def counted_bytes(rows: int, cols: int) -> int:
+        return rows * cols + rows * (cols // 32) * 8
+
     def get(self, key, raw: np.ndarray, rows: int, cols: int) -> Q8Matrix:
-        m = self._items.get(key)
-        if m is not None:
+        hit = self._items.get(key)
+        if hit is not None:
             self._items.move_to_end(key)
-            return m
+            return hit[0]
+        size = self.counted_bytes(rows, cols)
+        while self._items and self.held + size > self.budget:
+            _, (_, old_size) = self._items.popitem(last=False)
+            self.held -= old_size
         m = Q8Matrix.from_bytes(raw, rows, cols)
         self.uploads += 1
-        size = m.info()["bytes"]
-        self._items[key] = m
+        self._items[key] = (m, size)
         self.held += size
-        while self.held > self.budget and len(self._items) > 1:
-            _, old = self._items.popitem(last=False)
-            self.held -= old.info()["bytes"]
-            old.free()
         return m
 
+    def __len__(self):
+        return len(self._items)
+
+    def __contains__(self, key):
+        return key in self._items
+
     def clear(self):
-        for m in self._items.values():
-            m.free()
         self._items.clear()
         self.held = 0
 

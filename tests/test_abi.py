@@ -42,3 +42,10 @@ def test_layer_hash_is_sha256():
     for data in [b"", b"abc", b"a" * 55, b"a" * 56, b"a" * 64, bytes(range(256)) * 9] + longer:
         assert sha256(data) == hashlib.sha256(data).hexdigest()
     assert sha256(b"abc") == "ba7816bf8f01cfea414140de5dae2223b00361a396177a9cb410ff61f20015ad"
+
+
+def test_no_kernel_tracer_in_the_test_process():
+    # Graph replays are refused only under a kernel tracer; the tests run
+    # without one, so the graph cases run rather than being refused.
+    assert native.kernel_tracer_loaded() is False
+    assert "kernel tracer" in native.error_text(-7)

@@ -217,20 +217,27 @@ def test_gemma_embedding_scale_zero():
 
 @pytest.mark.parametrize("family,name", [("mistral-dense", "embed_tokens.weight"),
                                          ("gemma-dense", "embed_tokens_per_layer.weight")])
-def test_non_finite_embedding_scale_is_refused(family, name):
-    # q8.rs:45-47: a Q8_0 scale with exponent 0x1f is not finite; the
-    # embedding tables (read by row, not uploaded as matrices: an untied
-    # mistral-dense embedding, the gemma-dense per-layer one) are refused at
-    # upload, as the matrices are.
+def test_non_finite_embedding_row_is_refused_when_embedded(family, name):
+    # q8.rs:45-47: a Q8_0 scale with exponent 0x1f is not finite. The
+    # reference dequantizes embedding rows when a token is embedded
+    # (model.rs:316-330; the PLE prepare likewise), so a model with such a
+    # row loads and runs; a prompt holding that token is refused.
     if family == "mistral-dense":
         m = synth.mistral_model(128, 1, 4, 2, 32, 256, 512, seed=26)
     else:
         m = synth.tiny_gemma()
     t = m.tensors["model.language_model." + name].copy()
-    t[3, 0], t[3, 1] = 0x00, 0x7C  # +inf
+    t[3, 0], t[3, 1] = 0x00, 0x7C  # token 3's first block: +inf
     m.tensors["model.language_model." + name] = t
+    dm = DeviceModel(m)
+    s = Session(dm, 32, 8)
+    prompt = [5, 9, 2, 7]
+    got = s.generate(prompt, 1, keep_logits=True)
+    want_tokens, want_logits = _oracle_generate(m, prompt, 1, 32)
+    assert got.token_ids == want_tokens
+    assert np.array_equal(got.logits, np.stack(want_logits))
     with pytest.raises(native.IrisError) as e:
-        DeviceModel(m)
+        s.generate([5, 3, 2], 1)
     assert e.value.code == -2
 
 

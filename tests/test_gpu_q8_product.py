@@ -301,9 +301,14 @@ def test_per_block_scales_on_the_matrix_cores(kind, folds, tokens, rows, cols):
     assert m.info()["scale_mode"] == "f16"
     before = m.info()["bytes"]
     x = grouped_activations(rng, tokens, cols)
-    got = product_ws(m, x)
+    want = cpu.linear_q8(x, raw)
+    # Unprepared: the vector path, and the product allocates nothing.
+    assert np.array_equal(product_ws(m, x), want)
+    assert m.info()["bytes"] == before
+    m.prepare_matrix_cores()
     assert (m.info()["bytes"] > before) == folds  # the folded planes were built
-    assert np.array_equal(got, cpu.linear_q8(x, raw))
+    got = product_ws(m, x)
+    assert np.array_equal(got, want)
     # again, from the folded planes already there
     x2 = rand_activations(rng, 70, cols, 24)
     assert np.array_equal(product_ws(m, x2), cpu.linear_q8(x2, raw))
@@ -324,6 +329,7 @@ def test_per_block_gemm_at_the_benchmark_shape_sampled():
     raw = synth.q8_matrix(synth.tensor_seed(12, 1), rows, cols, synth.scale_base_for(cols), False)
     m = Q8Matrix.from_bytes(raw, rows, cols)
     assert m.info()["scale_mode"] == "f16"
+    m.prepare_matrix_cores()
     rng = np.random.default_rng(12)
     x = rng.integers(-(1 << 20), 1 << 20, (tokens, cols)).astype(np.int32)
     got = product_ws(m, x)

@@ -147,6 +147,30 @@ def test_layer_stage_matches_the_oracle(family):
     gap = stage.key_rows(keys[0][0][: a // 2], keys[0][1][: a // 2], 0)
     out = stage.run_layer_stage(s3, 0, acts, gap, ple)
     assert out.rows == [] and out.errors
+    if family == "gemma":
+        # A KV-shared layer's stage before its donor's stage over the same
+        # range: the donor's cache lacks the range's own keys, so the stage
+        # is refused rather than attending over stale keys.
+        layer = next(l for l in range(m.num_layers) if m.kv_donor_layer(l) >= 0)
+        src = m.kv_donor_layer(layer)
+        s4 = Session(dm, n, n)
+        s4.write_kv(src, 0, keys[src][0][:a], keys[src][1][:a])
+        acts = stage.ActivationSequence(
+            [stage.ActivationRow(int(t), rows[layer - 1][a + i].astype("<i4").tobytes())
+             for i, t in enumerate(ids[a:])], [], a)
+        ple = r._ple_rows(layer, list(ids[a:]), seed[a:])
+        prior = stage.key_rows(keys[layer][0][:a], keys[layer][1][:a], 0)
+        out = stage.run_layer_stage(s4, layer, acts, prior, ple)
+        assert out.rows == [] and out.errors
+        # after the donor's own stage over the range, the same stage runs
+        donor_acts = stage.ActivationSequence(
+            [stage.ActivationRow(int(t), (rows[src - 1] if src else seed)[a + i].astype("<i4").tobytes())
+             for i, t in enumerate(ids[a:])], [], a)
+        donor_prior = stage.key_rows(keys[src][0][:a], keys[src][1][:a], 0)
+        stage.run_layer_stage(s4, src, donor_acts, donor_prior, r._ple_rows(src, list(ids[a:]), seed[a:]))
+        out = stage.run_layer_stage(s4, layer, acts, prior, ple)
+        assert not out.errors and np.array_equal(out.values(), rows[layer][a:])
+        s4.free()
     for x in (s3, s2, s):
         x.free()
     dm.free()

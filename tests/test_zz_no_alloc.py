@@ -85,6 +85,14 @@ def test_one_token_and_per_block_scales():
         got = product_noalloc(m, x)
         assert np.array_equal(got, product_ws(m, x))
         assert np.array_equal(got, cpu.linear_q8(x, raw))
+    # folded for the matrix cores: the same values through both entry points
+    m.prepare_matrix_cores()
+    for tokens in (33, 5):
+        print(f"noalloc product: folded per-block scales, {tokens} tokens", flush=True)
+        x = activations(rng, tokens, cols, 20)
+        got = product_noalloc(m, x)
+        assert np.array_equal(got, product_ws(m, x))
+        assert np.array_equal(got, cpu.linear_q8(x, raw))
     m.free()
 
 
