@@ -9,7 +9,9 @@ constexpr uint32_t ATTN_MAX_KEYS = 65535;
 // Keys whose weights one workgroup holds in LDS at a time; longer views take
 // the tiled paths (scores re-read or re-formed per pass).
 constexpr uint32_t ATTN_TILE_KEYS = 4096;
-constexpr uint32_t ATTN_MAX_HEAD_DIM = 256;
+// Head sizes up to 512 (gemma-dense full-attention layers, global_head_dim
+// 512 in the reference's gemma-4 manifests).
+constexpr uint32_t ATTN_MAX_HEAD_DIM = 512;
 
 // Work space of the multi-row attention: the signed byte digits (four
 // planes) of the queries, keys and values in MFMA operand tiles, and the

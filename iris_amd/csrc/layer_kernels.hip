@@ -1,5 +1,6 @@
 // The non-product kernels of the token loop: exact attention over the
 // device KV cache and the prompt embedding gather.
+#include <algorithm>
 #include <map>
 #include <numeric>
 #include <mutex>
@@ -73,9 +74,13 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint
     }
     if (c * 64 > pos) return;
     const uint32_t kvh = head / (a.heads / a.kv_heads);
-    // The query element this thread stages, loaded first (waiting for it
-    // does not wait for the key loads issued after it).
-    const int32_t qv = a.q[(size_t)head * HD + tid % HD];
+    // The query elements this thread stages (one, or two for head size 512),
+    // loaded first (waiting for them does not wait for the key loads issued
+    // after them).
+    constexpr uint32_t QPT = HD > 256 ? HD / 256 : 1;
+    int32_t qv[QPT];
+#pragma unroll
+    for (uint32_t u = 0; u < QPT; u++) qv[u] = a.q[(size_t)head * HD + (tid + 256 * u) % HD];
     const uint32_t kq = lane & 15, grp = wave * 4 + (lane >> 4);
     const int32_t* kb = a.k_cache + ((size_t)kvh * HD + grp * DPG) * a.k_pos_stride + 4 * kq;
     int4 kv[DPG];
@@ -84,7 +89,9 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint
         for (uint32_t i = 0; i < DPG; i++) kv[i] = *(const int4*)(kb + (size_t)i * a.k_pos_stride + chunk * 64);
     };
     load_keys(c);
-    if (tid < HD) s_q[tid] = qv;
+#pragma unroll
+    for (uint32_t u = 0; u < QPT; u++)
+        if (tid + 256 * u < HD) s_q[tid + 256 * u] = qv[u];
     lds_barrier();
     for (;;) {
         uint64_t dot[4] = {0, 0, 0, 0};
@@ -474,12 +481,14 @@ int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys,
             case 64: return attention_decode_launch<64>(a, stream);
             case 128: return attention_decode_launch<128>(a, stream);
             case 256: return attention_decode_launch<256>(a, stream);
+            case 512: return attention_decode_launch<512>(a, stream);
             default: break;  // other head sizes: the one-workgroup-per-head kernel
         }
     }
     if (tokens >= 2 && iris_attention_prefill_applies(a, tokens, max_keys))
         return iris_attention_prefill_launch(a, tokens, max_keys, stream);
-    const uint32_t threads = tokens == 1 ? 1024 : 256;
+    // attend_row takes a multiple of 256 threads, at least one per head dimension.
+    const uint32_t threads = tokens == 1 ? 1024 : std::max(256u, (a.head_dim + 255) / 256 * 256);
     if (threads < a.head_dim || a.head_dim % 4) return IRIS_E_INVALID;
     hipLaunchKernelGGL(attention_kernel, dim3(a.heads, tokens), dim3(threads), 0, stream, a);
     return (int)hipGetLastError();

@@ -335,6 +335,22 @@ def tiny_gemma(seed=0x71E7) -> Model:
     return gemma_model(shape, 1024, seed=seed)
 
 
+def gemma4_e2b_scaled(seed=0x4E2B) -> Model:
+    """The Gemma-4-E2B layout (runtime/model-artifacts/gemma-4-E2B-q8/
+    manifest.json: 8 heads over 1 KV head, head size 256 on sliding layers
+    and 512 on full ones, partial rotary 0.25 on the full layers, sliding
+    window 512, KV-shared last layers, PLE width 256, softcap 30, RoPE bases
+    10000 / 1e6) at a smaller hidden size and depth: hidden 256, 7 layers
+    (four sliding, full, sliding, full; the last two KV-shared), GeGLU 512,
+    vocab 2048, tied head."""
+    shape = gemma_shape(256, 7, 8, 1, 256, 2048, 256, global_head_dim=512, sliding_window=512,
+                        layer_types=["sliding_attention"] * 4 + ["full_attention", "sliding_attention",
+                                                                 "full_attention"],
+                        num_kv_shared_layers=2, eps=1e-6, rope_sliding=10_000, rope_full=1_000_000,
+                        partial_rotary=0.25, softcap=30.0, tied_head=True)
+    return gemma_model(shape, 512, seed=seed)
+
+
 def gemma_2b(seed=0x2B2B) -> Model:
     """18 layers, hidden 2048, 8 heads of 256 with 1 KV head, GeGLU 16384,
     vocab 256000, RoPE base 10000, PLE width 256."""
