@@ -3,12 +3,13 @@ max_positions: crates/inference/kernels/src/mistral/layer.rs:121-127,
 prefill_range.rs:755-845), through the C ABI.
 
 Carried keys (iris_session_write_kv) fill every layer's cache up to a
-position near 4096; then a multi-row range whose rows see 4091..4110 keys
-(across the one-tile bound of the row routines) and one-row ranges past it
-(the decode kernels' tiled path) are compared with the oracle's layer over
-the same keys, fed the device's rows of the layer below. Two attention
-shapes: four query heads per KV head (the matrix-core prefill) and two (the
-one-row routine for every row).
+position near 4096, past 2^15, or near the session bound of 65535; then a
+multi-row range whose rows see the next 20 keys (the first case across the
+one-tile bound of the row routines) and one-row ranges past it (the decode
+kernels' tiled path) are compared with the oracle's layer over the same
+keys, fed the device's rows of the layer below. Two attention shapes: four
+query heads per KV head (the matrix-core prefill, whose exact value sums are
+held in int32 up to 2^16 keys) and two (the one-row routine for every row).
 """
 import numpy as np
 import pytest
@@ -19,7 +20,6 @@ from oracle import cpu
 
 pytestmark = pytest.mark.gpu
 
-CARRIED = 4090
 ROWS = 20
 DECODE = 3
 
@@ -29,10 +29,13 @@ def device():
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
 
 
-@pytest.mark.parametrize("heads,kv_heads", [(8, 2), (4, 2)])
-def test_views_longer_than_one_tile_match_the_oracle(heads, kv_heads):
-    m = synth.mistral_model(256, 2, heads, kv_heads, 64, 512, 1024, seed=71 + heads)
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("heads,kv_heads,CARRIED", [(8, 2, 4090), (4, 2, 4090), (8, 2, 40000), (8, 2, 65500),
+                                                    (4, 2, 65500)])
+def test_views_longer_than_one_tile_match_the_oracle(heads, kv_heads, CARRIED):
+    m = synth.mistral_model(256, 2, heads, kv_heads, 64, 512, 1024, seed=71 + heads, max_positions=65536)
     n = CARRIED + ROWS + DECODE
+    assert n <= 65535
     ids = synth.token_ids(72, n, m.vocab)
     kvw = kv_heads * 64
     rng = np.random.default_rng(73)
