@@ -24,7 +24,10 @@ The JSON line also carries:
   and out of every call, as the reference's gpu.rs calls it) timed per call
   for the microbenchmark's GEMV and GEMM, the matrix already uploaded;
 - cpu_baseline: the CPU oracle (a C restatement of the reference's kernels)
-  timed on a bounded sample of the same decode on this host's cores.
+  timed on a bounded sample of the same decode on this host's cores;
+- measured_peaks: the part's HBM read rate (a plain streaming kernel over
+  1 GiB) and int8 matrix-core rate (independent 32x32x32 MFMAs, constant
+  and random operands), beside the vendor figures the fractions use.
 """
 from __future__ import annotations
 
@@ -182,6 +185,10 @@ def main():
 
     roof = gemv_roofline(decode_timing)
     log(f"GEMV {roof['avg_launch_us']} us = {roof['achieved']} GB/s ({100 * roof['frac']:.1f}% of peak)")
+    peaks = decode_timing.measured_peaks()
+    roof["frac_of_measured_stream"] = round(roof["achieved"] / peaks["hbm_read_gbps"], 4)
+    log(f"measured peaks: HBM read {peaks['hbm_read_gbps']} GB/s; int8 MFMA {peaks['mfma_i8_tops_constant']} TOP/s "
+        f"constant operands, {peaks['mfma_i8_tops_random']} random")
     gpb = decode_timing.time_gemv(per_row_scale=False)
     gemv_pb = {"launch": "Q8_0 GEMV M=1 K=4096 N=14336, one f16 scale per block",
                "avg_launch_us": round(gpb["us"], 3), "algorithmic_bytes": gpb["algorithmic_bytes"],
@@ -196,6 +203,7 @@ def main():
     log(f"teacher-forced {TEACHER_FORCED_ROWS} rows: pass {tf['pass_ms']} ms, with checkpoints {tf['checkpoint_ms']} ms")
     bench.dm.free()
     gemm = decode_timing.time_gemm(TEACHER_FORCED_ROWS)
+    gemm["frac_of_measured_random"] = round(gemm["mfma_tops"] / peaks["mfma_i8_tops_random"], 4)
     log(f"MFMA GEMM {gemm['shape']}: {gemm['us']} us = {gemm['mfma_tops']} TOP/s ({100 * gemm['frac']:.1f}% of int8 peak)")
     # The isolated product microbenchmark's GEMM: M=512, K=N=4096, row scales,
     # activations a * s_t (a in [-127, 127], s_t = 2^8 + random % 2^8).
@@ -245,6 +253,7 @@ def main():
                    "prompt_tokens": PROMPT, "decode_steps_timed": args.steps, "batch": 1,
                    "decode_launches": "direct" if args.direct_launches else "graph replay"},
         "roofline": roof,
+        "measured_peaks": peaks,
         "gemv_per_block": gemv_pb,
         "c2_gemm": c2,
         "pcie_inclusive": pcie,

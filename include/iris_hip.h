@@ -149,6 +149,19 @@ int iris_time_product(const Q8GpuMatrix* const* matrices, uint32_t count, const 
 int iris_time_product_ws(const Q8GpuMatrix* matrix, const int32_t* d_activations, uint32_t tokens, int32_t* d_out,
                          void* d_workspace, uint64_t workspace_bytes, uint32_t iterations, double* ms_per_product);
 
+/* Measured peaks of the device (no counterpart in the reference; reported
+ * beside the vendor figures). iris_probe_hbm_read: the read rate of a plain
+ * streaming kernel (16-byte loads at a grid stride, the best of a few grid
+ * sizes) over `bytes` of device memory at d_buf (16-byte aligned; larger
+ * than the last-level cache for an HBM figure), averaged over `repeats`
+ * passes, in GB/s. iris_probe_mfma_i8: the rate of v_mfma_i32_32x32x32_i8 in
+ * a loop of independent accumulators on every SIMD (four waves per SIMD),
+ * `iterations` (at least 4) instructions per accumulator, in TOP/s, with
+ * constant operands (random_operands = 0) or with random operands that
+ * change every instruction (1). */
+int iris_probe_hbm_read(const void* d_buf, uint64_t bytes, uint32_t repeats, double* gb_per_s);
+int iris_probe_mfma_i8(uint32_t random_operands, uint32_t iterations, double* tops);
+
 /* ------------------------------------------------------------------------
  * The deterministic token loop, device-resident.
  *

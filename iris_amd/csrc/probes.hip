@@ -1,0 +1,163 @@
+// Measured peaks of the part, reported beside the vendor figures: the HBM
+// read rate of a plain streaming kernel, and the int8 matrix-core rate of a
+// loop of independent v_mfma_i32_32x32x32_i8 on constant or on changing
+// random operands (the matrix cores' clock falls under switching
+// operands, so the second is the ceiling the exact products can meet).
+#include <algorithm>
+
+#include "q8_internal.h"
+
+namespace {
+
+constexpr uint32_t STREAM_THREADS = 256;
+constexpr uint32_t STREAM_UNROLL = 4;  // 16-byte loads in flight per thread
+
+// Every thread reads 16-byte words at a grid stride, STREAM_UNROLL at a
+// time, and folds them with xor; one word per workgroup is written only if
+// the fold hits a value no real buffer gives, so the loads are not dead.
+__global__ __launch_bounds__(STREAM_THREADS) void stream_read_kernel(const uint4* buf, uint64_t words, uint32_t* out) {
+    const uint64_t stride = (uint64_t)gridDim.x * STREAM_THREADS;
+    uint32_t acc = 0;
+    uint64_t i = (uint64_t)blockIdx.x * STREAM_THREADS + threadIdx.x;
+    for (; i + (STREAM_UNROLL - 1) * stride < words; i += STREAM_UNROLL * stride) {
+        uint4 v[STREAM_UNROLL];
+#pragma unroll
+        for (uint32_t u = 0; u < STREAM_UNROLL; u++) v[u] = buf[i + u * stride];
+#pragma unroll
+        for (uint32_t u = 0; u < STREAM_UNROLL; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < words; i += stride) {
+        const uint4 v = buf[i];
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    if (acc == 0x9E3779B9u) out[blockIdx.x] = acc;
+}
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+constexpr uint32_t MFMA_CHAINS = 4;  // independent accumulators per wave
+constexpr uint32_t MFMA_ROT = 4;     // operand pairs cycled (random operands)
+constexpr uint32_t MFMA_OPS = 2 * 32 * 32 * 32;
+
+__device__ __forceinline__ uint32_t mix32(uint32_t x) {
+    x ^= x >> 16;
+    x *= 0x7feb352du;
+    x ^= x >> 15;
+    x *= 0x846ca68bu;
+    return x ^ (x >> 16);
+}
+
+// `rounds` x MFMA_ROT rounds of MFMA_CHAINS independent 32x32x32 int8
+// MFMAs per wave. RANDOM: MFMA_ROT operand pairs of random bytes, cycled
+// (the unrolled rotation keeps the indexing static), so the operands change
+// every instruction; else one constant pair.
+template <bool RANDOM>
+__global__ __launch_bounds__(256) void mfma_i8_kernel(uint32_t rounds, uint32_t* out) {
+    const uint32_t seed = (blockIdx.x * 256 + threadIdx.x) * 0x9E3779B9u;
+    v4i a[MFMA_ROT], b[MFMA_ROT];
+#pragma unroll
+    for (uint32_t k = 0; k < MFMA_ROT; k++)
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            a[k][c] = RANDOM ? (int)mix32(seed + 8 * k + c) : 0x01020304;
+            b[k][c] = RANDOM ? (int)mix32(seed + 8 * k + 4 + c + 0x5bd1e995u) : 0x05060708;
+        }
+    v16i acc[MFMA_CHAINS];
+#pragma unroll
+    for (uint32_t c = 0; c < MFMA_CHAINS; c++) acc[c] = v16i{};
+    for (uint32_t it = 0; it < rounds; it++) {
+#pragma unroll
+        for (uint32_t r = 0; r < MFMA_ROT; r++)
+#pragma unroll
+            for (uint32_t c = 0; c < MFMA_CHAINS; c++)
+                acc[c] = __builtin_amdgcn_mfma_i32_32x32x32_i8(a[(r + c) % MFMA_ROT], b[(r + 2 * c + 1) % MFMA_ROT],
+                                                               acc[c], 0, 0, 0);
+    }
+    int s = 0;
+#pragma unroll
+    for (uint32_t c = 0; c < MFMA_CHAINS; c++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) s ^= acc[c][e];
+    if ((uint32_t)s == 0x9E3779B9u) out[blockIdx.x] = (uint32_t)s;
+}
+
+template <class Launch>
+int time_launches(Launch&& launch, uint32_t repeats, double* ms_per_launch) {
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t st = hipEventCreate(&e0);
+    if (st == hipSuccess) st = hipEventCreate(&e1);
+    if (st == hipSuccess) {
+        launch();  // warm-up
+        st = hipGetLastError();
+    }
+    if (st == hipSuccess) st = hipEventRecord(e0, nullptr);
+    for (uint32_t r = 0; st == hipSuccess && r < repeats; r++) {
+        launch();
+        st = hipGetLastError();
+    }
+    if (st == hipSuccess) st = hipEventRecord(e1, nullptr);
+    if (st == hipSuccess) st = hipEventSynchronize(e1);
+    float ms = 0.f;
+    if (st == hipSuccess) st = hipEventElapsedTime(&ms, e0, e1);
+    if (st == hipSuccess) *ms_per_launch = (double)ms / repeats;
+    if (e0) hipEventDestroy(e0);
+    if (e1) hipEventDestroy(e1);
+    return (int)st;
+}
+
+}  // namespace
+
+extern "C" int iris_probe_hbm_read(const void* d_buf, uint64_t bytes, uint32_t repeats, double* gb_per_s) {
+    if (!d_buf || !gb_per_s || repeats == 0 || bytes < 16 || ((uintptr_t)d_buf & 15)) return IRIS_E_INVALID;
+    const int cus = iris_device_cus();
+    // The best of a few grid sizes (2, 4 and 32 workgroups of 256 threads
+    // per CU; two has been the fastest on this part).
+    const uint32_t per_cu[] = {2, 4, 32};
+    uint32_t* out = nullptr;
+    hipError_t st = hipMalloc((void**)&out, (size_t)cus * 32 * 4);
+    if (st != hipSuccess) return (int)st;
+    const uint64_t words = bytes / 16;
+    double best = 0;
+    int rc = 0;
+    for (uint32_t k : per_cu) {
+        const uint32_t wgs = (uint32_t)cus * k;
+        double ms = 0;
+        rc = time_launches(
+            [&] {
+                hipLaunchKernelGGL(stream_read_kernel, dim3(wgs), dim3(STREAM_THREADS), 0, nullptr,
+                                   (const uint4*)d_buf, words, out);
+            },
+            repeats, &ms);
+        if (rc != 0) break;
+        best = std::max(best, (double)(words * 16) / (ms * 1e-3) / 1e9);
+    }
+    hipFree(out);
+    if (rc == 0) *gb_per_s = best;
+    return rc;
+}
+
+extern "C" int iris_probe_mfma_i8(uint32_t random_operands, uint32_t iterations, double* tops) {
+    if (!tops || iterations < MFMA_ROT) return IRIS_E_INVALID;
+    const int cus = iris_device_cus();
+    const uint32_t wgs = (uint32_t)cus * 4;  // four 4-wave workgroups per CU: four waves per SIMD
+    const uint32_t rounds = iterations / MFMA_ROT;
+    uint32_t* out = nullptr;
+    hipError_t st = hipMalloc((void**)&out, (size_t)wgs * 4);
+    if (st != hipSuccess) return (int)st;
+    double ms = 0;
+    int rc = time_launches(
+        [&] {
+            if (random_operands)
+                hipLaunchKernelGGL(mfma_i8_kernel<true>, dim3(wgs), dim3(256), 0, nullptr, rounds, out);
+            else
+                hipLaunchKernelGGL(mfma_i8_kernel<false>, dim3(wgs), dim3(256), 0, nullptr, rounds, out);
+        },
+        3, &ms);
+    hipFree(out);
+    if (rc == 0) {
+        const double ops = (double)wgs * 4 * rounds * MFMA_ROT * MFMA_CHAINS * MFMA_OPS;
+        *tops = ops / (ms * 1e-3) / 1e12;
+    }
+    return rc;
+}

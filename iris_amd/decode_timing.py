@@ -337,6 +337,28 @@ def eager_decode(steps: int, gemma: bool = False) -> dict:
             "wall_s": round(wall, 3)}
 
 
+def measured_peaks(stream_bytes: int = 1 << 30) -> dict:
+    """The part's measured peaks, beside the vendor figures (8 TB/s HBM,
+    5.0 POP/s dense int8): the read rate of a plain streaming kernel over
+    `stream_bytes` (four times the last-level cache, so every pass comes
+    from HBM), and the int8 matrix-core rate of a loop of independent
+    32x32x32 MFMAs with constant operands and with random operands that
+    change every instruction (the matrix cores' clock drops under switching
+    operands; the exact products' operands are random)."""
+    L = native.lib()
+    buf = native.DeviceBuffer(stream_bytes)
+    native.check(L.iris_memcpy_h2d(buf.ptr, np.zeros(1 << 20, dtype=np.uint8).ctypes.data, 1 << 20), "fill")
+    gbps = C.c_double()
+    native.check(L.iris_probe_hbm_read(buf.ptr, stream_bytes, 20, C.byref(gbps)), "HBM read probe")
+    buf.free()
+    out = {"hbm_read_gbps": round(gbps.value, 1), "hbm_stream_bytes": stream_bytes}
+    for name, rnd in (("mfma_i8_tops_constant", 0), ("mfma_i8_tops_random", 1)):
+        t = C.c_double()
+        native.check(L.iris_probe_mfma_i8(rnd, 20000, C.byref(t)), "MFMA probe")
+        out[name] = round(t.value, 1)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
     ap.add_argument("--steps", type=int, default=PROMPT - 1)
@@ -359,6 +381,8 @@ def main(argv=None):
                     help="only a decode of STEPS steps launched from the host, no graph (for traces and "
                          "counters); Mistral-7B shape, or Gemma-2B shape with --gemma")
     ap.add_argument("--gemma", action="store_true", help="with --eager-decode: the Gemma-2B shape")
+    ap.add_argument("--peaks", action="store_true",
+                    help="only the measured peaks: HBM read stream and int8 MFMA (constant and random operands)")
     args = ap.parse_args(argv)
     global USE_GRAPH
     if USE_GRAPH and native.kernel_tracer_loaded():
@@ -366,6 +390,9 @@ def main(argv=None):
         print("kernel tracer loaded: decodes launched one by one", file=sys.stderr, flush=True)
         USE_GRAPH = False
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
+    if args.peaks:
+        print(json.dumps(measured_peaks()), flush=True)
+        return
     if args.eager_decode:
         print(json.dumps(eager_decode(args.eager_decode, args.gemma)), flush=True)
         return
