@@ -62,3 +62,72 @@ def test_q8_exact_blocks():
     assert half[:2] == bytes([0x00, 0x38]) and half[2] == 1
     with pytest.raises(ValueError):
         fx.q8_exact([1] * 31 + [fx.ONE * 200])
+
+
+def test_gemma_layer_known_answer_through_the_whole_layer():
+    # native_decode_rotary_outputs_match_prefill_across_chunks
+    # (crates/inference/direct/tests/executor.rs:190-350): one gemma-dense
+    # layer, 32 wide, every product the identity (exact Q8_0, and Q16.16 for
+    # the PLE matrices), norms ONE, q/k norms the one-hot e0, RoPE base
+    # 10000 on the first pair (rotary 2, frequency base 2), over five rows
+    # of ONE with lane 1 at +-ONE: position 1's cached key starts
+    # [35408, 55146] (:316-319). This pins the layer's key path end to end:
+    # input norm, product, k norm, rotation, cache store. The same layer
+    # over the chunks (0,1), (1,2), (2,3), (3,5) reproduces the one pass's
+    # rows and keys (:322-346).
+    import ctypes as C
+    W = fx.W
+    ONE = fx.ONE
+    identity = fx.one_hot_rows(range(W))
+    q8_id = np.frombuffer(fx.q8_exact(identity), dtype=np.uint8).reshape(W, 34)
+    i32_id = np.asarray(identity, dtype=np.int32).reshape(W, W)
+    keep = []
+
+    def hold(a, dtype):
+        a = np.ascontiguousarray(a, dtype=dtype)
+        keep.append(a)
+        return a.ctypes.data
+
+    L = cpu.GemmaLayerC()
+    L.hidden = L.ffn = W
+    L.heads = L.kv_heads = 1
+    L.head_dim = W
+    L.ple_width = W
+    L.sliding_window = 0
+    L.layer_scalar = 0
+    L.norm_eps = 0
+    L.rope_base = 10_000 << 32
+    L.rotary_dim = 2
+    L.rope_freq_base_dim = 2
+    norm = [ONE] * W
+    unit = fx.one_hot_rows([0])
+    for f in ("norm_input", "norm_post_attn", "norm_pre_ffw", "norm_post_ffw", "ple_post_norm"):
+        setattr(L, f, hold(norm, np.int32))
+    L.q_norm = hold(unit, np.int32)
+    L.k_norm = hold(unit, np.int32)
+    for f in ("w_q", "w_k", "w_v", "w_o", "w_gate", "w_up", "w_down"):
+        setattr(L, f, hold(q8_id, np.uint8))
+    L.ple_input_gate = hold(i32_id, np.int32)
+    L.ple_layer_projection = hold(i32_id, np.int32)
+
+    rows = np.full((5, W), ONE, dtype=np.int32)
+    rows[1::2, 1] = -ONE
+    ple = np.full((5, W), ONE, dtype=np.int32)
+
+    def run(x, start, k, v):
+        out = np.empty_like(x)
+        rc = cpu.lib().orc_gemma_layer_forward(C.byref(L), np.ascontiguousarray(x), x.shape[0], start, k, v, k, v,
+                                              np.ascontiguousarray(ple[start:start + x.shape[0]]), out, 1)
+        assert rc == 0
+        return out
+
+    k_all = np.zeros((8, W), dtype=np.int32)
+    v_all = np.zeros((8, W), dtype=np.int32)
+    whole = run(rows, 0, k_all, v_all)
+    assert list(k_all[1][:2]) == [35408, 55146]
+    k = np.zeros((8, W), dtype=np.int32)
+    v = np.zeros((8, W), dtype=np.int32)
+    for a, b in [(0, 1), (1, 2), (2, 3), (3, 5)]:
+        got = run(rows[a:b], a, k, v)
+        assert np.array_equal(got, whole[a:b]), (a, b)
+        assert np.array_equal(k[:b], k_all[:b]) and np.array_equal(v[:b], v_all[:b]), (a, b)
