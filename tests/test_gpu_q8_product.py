@@ -232,15 +232,17 @@ def test_mfma_product_digit_paths(tokens, rows, cols):
 
 
 def test_mfma_product_wide_row_scales():
-    # Row-scale matrices whose Q.24 scales reach f16 exponent 30 (about 2^40),
-    # both signs, against full-range activations with every magnitude from 8
-    # to 32 bits: the MFMA epilogue's 64-bit rounding path, its bit-length
-    # test near 2^63 and its 128-bit redo all run; every output is compared.
+    # Row-scale matrices whose Q.24 scales run from zero and subnormals up to
+    # f16 exponent 30 (about 2^40), both signs, against full-range
+    # activations with every magnitude from 8 to 32 bits: the MFMA epilogue's
+    # 64-bit rounding path, its bit-length test near 2^63 and its 128-bit
+    # redo all run; every output is compared.
     rng = np.random.default_rng(31)
     rows, cols, tokens = 512, 1024, 96
     nb = cols // 32
-    exponent = np.concatenate([rng.integers(1, 12, 128), rng.integers(12, 22, 128), rng.integers(22, 31, 256)])
+    exponent = np.concatenate([rng.integers(0, 12, 128), rng.integers(12, 22, 128), rng.integers(22, 31, 256)])
     bits = ((rng.integers(0, 2, rows) << 15) | (exponent << 10) | rng.integers(0, 1024, rows)).astype(np.int64)
+    bits[:3] = [0, 0x8000, 0x0001]  # zero, negative zero, the smallest subnormal
     raw = np.empty((rows, nb, 34), np.uint8)
     raw[:, :, 0] = (bits & 0xFF)[:, None]
     raw[:, :, 1] = (bits >> 8)[:, None]
