@@ -9,6 +9,9 @@ constexpr uint32_t ATTN_MAX_KEYS = 65535;
 // Keys whose weights one workgroup holds in LDS at a time; longer views take
 // the tiled paths (scores re-read or re-formed per pass).
 constexpr uint32_t ATTN_TILE_KEYS = 4096;
+// Scores workgroups per query head of a one-row launch, at most (longer
+// views loop over 64-position chunks).
+constexpr uint32_t ATTN_DECODE_CHUNKS = 32;
 // Head sizes up to 512 (gemma-dense full-attention layers, global_head_dim
 // 512 in the reference's gemma-4 manifests).
 constexpr uint32_t ATTN_MAX_HEAD_DIM = 512;
@@ -39,6 +42,11 @@ inline uint64_t attn_e_store_bytes(uint32_t heads, uint32_t qt_cap, uint32_t ks_
     return 4096ull * heads * qt_cap * ks_cap;
 }
 
+// int32 elements of AttnArgs::scores for `heads` query heads.
+inline uint64_t attn_scores_ints(uint32_t heads, uint32_t k_pos_stride) {
+    return (uint64_t)heads * k_pos_stride + 2ull * heads * ATTN_DECODE_CHUNKS;
+}
+
 struct AttnArgs {
     const int32_t* q;        // [tokens][heads*head_dim]
     uint32_t q_stride;
@@ -54,7 +62,9 @@ struct AttnArgs {
     uint32_t scale_q32;
     uint32_t window;         // 0 = every earlier position is visible
     // One-row launches: the head's scores between the two decode kernels,
-    // [heads][k_pos_stride] (null: the one-workgroup-per-head kernel).
+    // [heads][k_pos_stride], then each scores workgroup's first maximum,
+    // [heads][ATTN_DECODE_CHUNKS] 64-bit keys; attn_scores_ints elements
+    // (null: the one-workgroup-per-head kernel).
     int32_t* scores;
     // Digit planes for the multi-row MFMA path (planes.q null: the scalar
     // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes /

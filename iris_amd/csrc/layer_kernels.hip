@@ -22,11 +22,12 @@ __global__ __launch_bounds__(ATTN_MAX_THREADS) void attention_kernel(const AttnA
 // (query head, 64-position chunk of the cache) forms the chunk's scores
 // (wrapping i64 dot, then scaled_score or requantize) into a.scores; each
 // workgroup reads only its chunk's keys, so the key bytes a head needs are
-// spread over many compute units. (2) attn_values_kernel: one workgroup per
-// (query head, 32-dimension slice) reads the head's scores, finds the first
-// maximum, forms the exp terms, their sum and the weights, then the weighted
-// values of its slice over every key; the slice's value loads are issued
-// first and stay in flight through the softmax.
+// spread over many compute units; each workgroup also leaves the first
+// maximum of its keys. (2) attn_values_kernel: one workgroup per (query
+// head, 32-dimension slice) takes the head's first maximum from those, reads
+// the head's scores, forms the exp terms, their sum and the weights, then
+// the weighted values of its slice over every key; the slice's value loads
+// are issued right after the scores and stay in flight through the softmax.
 
 // Thread (position quad kq, dimension group grp of 16) holds HD/16 dimensions
 // of four consecutive positions: one 16-byte load per dimension from the
@@ -54,8 +55,25 @@ __device__ __forceinline__ uint2 xcd_head_order(const AttnArgs& a, uint32_t L, u
     return make_uint2((u % a.kv_heads) * group + r, u / a.kv_heads);
 }
 
+// The first maximum of scores as 64-bit keys: the score with its sign bit
+// flipped, then the complemented key index from the view's start, so that
+// the larger key is the larger score and, among equal scores, the lower
+// index (0 = no key).
+__device__ __forceinline__ uint64_t max_key(int32_t score, uint32_t j) {
+    return ((uint64_t)((uint32_t)score ^ 0x80000000u) << 32) | (uint32_t)~j;
+}
+__device__ __forceinline__ ArgMax from_max_key(uint64_t k) {
+    return ArgMax{(int32_t)((uint32_t)(k >> 32) ^ 0x80000000u), ~(uint32_t)k};
+}
+// Each scores workgroup's first maximum, [heads][ATTN_DECODE_CHUNKS], after
+// the scores (k_pos_stride is a multiple of 64: 256-byte aligned).
+__device__ __forceinline__ uint64_t* chunk_maxima(const AttnArgs& a) {
+    return (uint64_t*)(a.scores + (size_t)a.heads * a.k_pos_stride);
+}
+
 // Workgroup (head, y) takes the 64-position chunks y, y + chunks, ... of
-// the view (one chunk each for views up to 64 * chunks keys).
+// the view (one chunk each for views up to 64 * chunks keys), and leaves
+// the first maximum of its visible keys in chunk_maxima.
 template <uint32_t HD>
 __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint32_t chunks) {
     constexpr uint32_t DPG = HD / 16;
@@ -65,6 +83,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint
     const uint32_t head = hy.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
+    uint64_t* max_out = chunk_maxima(a) + (size_t)head * ATTN_DECODE_CHUNKS + hy.y;
     // The first chunk of this workgroup that holds a visible key (every
     // later one up to the position does too).
     uint32_t c = hy.y;
@@ -72,7 +91,10 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint
         const uint32_t behind = start - (c * 64 + 63), step = 64 * chunks;
         c += (behind + step - 1) / step * chunks;
     }
-    if (c * 64 > pos) return;
+    if (c * 64 > pos) {
+        if (tid == 0) *max_out = 0;  // no key
+        return;
+    }
     const uint32_t kvh = head / (a.heads / a.kv_heads);
     // The query elements this thread stages (one, or two for head size 512),
     // loaded first (waiting for them does not wait for the key loads issued
@@ -93,6 +115,7 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint
     for (uint32_t u = 0; u < QPT; u++)
         if (tid + 256 * u < HD) s_q[tid + 256 * u] = qv[u];
     lds_barrier();
+    uint64_t best = 0;  // wave 0: the first maximum of the visible keys so far
     for (;;) {
         uint64_t dot[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -120,43 +143,112 @@ __global__ __launch_bounds__(256) void attn_scores_kernel(const AttnArgs a, uint
             const int32_t sc =
                 a.scaled ? dn::scaled_score_from_sum((int64_t)sum, a.scale_q32) : dn::requantize((int64_t)sum);
             a.scores[(size_t)head * a.k_pos_stride + c0 + tid] = sc;  // positions outside the view are never read
+            const uint32_t p = c0 + tid;
+            const uint64_t k = max_key(sc, p - start);
+            best = ((p >= start) & (p <= pos) & (k > best)) ? k : best;
         }
         if (!more) break;
         lds_barrier();  // s_part is read before the next chunk overwrites it
     }
+    if (wave == 0) {
+        best = wave_max_u64(best);
+        if (lane == 0) *max_out = best;
+    }
 }
 
 constexpr uint32_t VAL_NT = 512, VAL_NW = VAL_NT / 64;
-constexpr uint32_t VAL_DS = 32;  // dimensions per values workgroup
+constexpr uint32_t VAL_DS = 32;                // dimensions per values workgroup
+constexpr uint32_t VAL_TPR = VAL_DS / 4;       // threads per value row, four dimensions each
+constexpr uint32_t VAL_RP = VAL_NT / VAL_TPR;  // value rows one pass of the workgroup reads
 
 struct ValuesSmem {
     int32_t w[ATTN_TILE_KEYS];  // weights
-    int64_t part[64 * VAL_DS];
-    ArgMax am[VAL_NW];
+    int64_t part[VAL_NW][VAL_DS];
     uint64_t sum[VAL_NW];
     int32_t wsum[VAL_NW];
 };
 
-// The values workgroup for a view longer than ATTN_TILE_KEYS: the first
-// maximum and the exp sum from the stored scores (two reads), then tile by
-// tile the weights (exp terms formed again) and their weighted values. The
-// first maximum's residual is added at the end as resid * v: the weighted
-// sum is linear and wraps, so this equals the reference's adjusted weight.
+// The head's first maximum from the scores workgroups' maxima, in every
+// wave (no barrier): lane i < chunks holds workgroup i's key.
+__device__ __forceinline__ ArgMax head_first_max(uint64_t lane_key) {
+    return from_max_key(wave_max_u64(lane_key));
+}
+
+// Weighted values in f64, exactly: the weights are non-negative, each at
+// most 2^16 + 1, and sum to at most 2^16 plus one half per key (under 2^17
+// for ATTN_MAX_KEYS keys), and |v| <= 2^31, so every product and every
+// partial sum of any subset of keys is an integer below 2^48 in magnitude:
+// each fma is exact and the sum equals the reference's wrapping i64 sum
+// (which never wraps). v_fma_f64 issues at full rate where the i64
+// multiply-add is a quarter-rate instruction.
+__device__ __forceinline__ void weigh_values(double (&acc)[4], int32_t w, int4 v) {
+    const double wd = (double)w;
+    acc[0] = fma(wd, (double)v.x, acc[0]);
+    acc[1] = fma(wd, (double)v.y, acc[1]);
+    acc[2] = fma(wd, (double)v.z, acc[2]);
+    acc[3] = fma(wd, (double)v.w, acc[3]);
+}
+
+// The slice's value at the first maximum (thread t: dimension t % VAL_DS),
+// loaded as soon as the maximum is known; unconditional, since a
+// conditional load is waited for, with every load before it, where its
+// branch joins.
 template <uint32_t HD>
-__device__ void values_long(const AttnArgs& a, ValuesSmem& sm, uint32_t head, uint32_t slice, uint32_t kvh,
-                            uint32_t start, uint32_t n) {
+__device__ __forceinline__ int32_t first_max_value(const AttnArgs& a, ArgMax m, uint32_t slice, uint32_t kvh,
+                                                   uint32_t start) {
+    return a.v_cache[(size_t)(start + m.i) * a.kv_stride + (size_t)kvh * HD + slice * VAL_DS + threadIdx.x % VAL_DS];
+}
+
+// The end of a values workgroup: acc holds this thread's weighted values of
+// dimensions d4..d4+3 over its value rows (exact integers, see
+// weigh_values), wpart the wave's sum of weights, vmax the first maximum's
+// value (first_max_value). The rows meet across the wave's lanes (lanes
+// equal modulo VAL_TPR share dimensions), then across the waves in LDS, in
+// wrapping i64; thread d < VAL_DS adds the first maximum's residual weight
+// times its value (add_sat(w, ONE - sum) at the first maximum: no
+// saturation at these magnitudes, so the change is + (ONE - sum) * v) and
+// requantizes.
+template <uint32_t HD>
+__device__ __forceinline__ void values_finish(const AttnArgs& a, ValuesSmem& sm, const double (&accd)[4],
+                                              int32_t wpart, int32_t vmax, uint32_t head, uint32_t slice) {
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int32_t* sb = a.scores + (size_t)head * a.k_pos_stride + start;
-    uint64_t best = 0;
-    for (uint32_t j = tid; j < n; j += VAL_NT) {
-        const uint64_t k = ((uint64_t)((uint32_t)sb[j] ^ 0x80000000u) << 32) | (uint32_t)~j;
-        best = k > best ? k : best;
+    uint64_t acc[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) acc[c] = (uint64_t)(int64_t)accd[c];
+#pragma unroll
+    for (uint32_t off = VAL_TPR; off < 64; off <<= 1)
+#pragma unroll
+        for (int c = 0; c < 4; c++) acc[c] += __shfl_xor(acc[c], off);
+    if (lane < VAL_TPR)
+#pragma unroll
+        for (int c = 0; c < 4; c++) sm.part[wave][lane * 4 + c] = (int64_t)acc[c];
+    if (lane == 0) sm.wsum[wave] = wpart;
+    lds_barrier();
+    if (tid < VAL_DS) {
+        // Weights are non-negative and sum to 2^16 plus at most one half per
+        // key: the saturating sum never saturates, a plain sum is the same.
+        int32_t wsum = 0;
+        uint64_t t = 0;
+#pragma unroll
+        for (uint32_t i = 0; i < VAL_NW; i++) {
+            wsum = dn::add_sat(wsum, sm.wsum[i]);
+            t += (uint64_t)sm.part[i][tid];
+        }
+        const int64_t resid = dn::sub_sat(dn::ONE_ACT, wsum);
+        t += (uint64_t)(resid * vmax);
+        a.ctx[(size_t)head * HD + slice * VAL_DS + tid] = dn::requantize((int64_t)t);
     }
-    best = wave_max_u64(best);
-    if (lane == 0) sm.am[wave] = ArgMax{(int32_t)((uint32_t)(best >> 32) ^ 0x80000000u), ~(uint32_t)best};
-    __syncthreads();
-    ArgMax m = sm.am[0];
-    for (uint32_t i = 1; i < VAL_NW; i++) m = argmax_combine(m, sm.am[i]);
+}
+
+// The values workgroup for a view longer than ATTN_TILE_KEYS: the exp sum
+// from the stored scores, then tile by tile the weights (exp terms formed
+// again) and their weighted values.
+template <uint32_t HD>
+__device__ void values_long(const AttnArgs& a, ValuesSmem& sm, ArgMax m, uint32_t head, uint32_t slice,
+                            uint32_t kvh, uint32_t start, uint32_t n) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int32_t vmax = first_max_value<HD>(a, m, slice, kvh, start);
+    const int32_t* sb = a.scores + (size_t)head * a.k_pos_stride + start;
     auto exp_term = [&](uint32_t j) -> uint64_t {
         const int64_t diff = (int64_t)m.v - sb[j];
         return diff < (1 << 20) ? dn::softmax_exp_diff((uint32_t)diff) : 0;
@@ -170,11 +262,10 @@ __device__ void values_long(const AttnArgs& a, ValuesSmem& sm, uint32_t head, ui
     uint64_t total = 0;
     for (uint32_t i = 0; i < VAL_NW; i++) total += sm.sum[i];
     const double w_scale = 65536.0 / (double)total, q_scale = 4294967296.0 / (double)total;
-    const uint32_t kr = tid / 8, d4 = (tid % 8) * 4;
+    const uint32_t kr = tid / VAL_TPR, d4 = (tid % VAL_TPR) * 4;
     const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * HD + slice * VAL_DS + d4;
-    // The weights sum to 2^16 plus at most one half per key: a plain sum.
     int32_t wpart = 0;
-    uint64_t acc[4] = {0, 0, 0, 0};
+    double acc[4] = {0, 0, 0, 0};
     for (uint32_t t0 = 0; t0 < n; t0 += ATTN_TILE_KEYS) {
         const uint32_t tn = min(ATTN_TILE_KEYS, n - t0);
         for (uint32_t j = tid; j < tn; j += VAL_NT) {
@@ -183,58 +274,39 @@ __device__ void values_long(const AttnArgs& a, ValuesSmem& sm, uint32_t head, ui
             wpart += w;
         }
         __syncthreads();
-        for (uint32_t key = kr; key < tn; key += 64) {
-            const int4 v = *(const int4*)(vb + (size_t)(t0 + key) * a.kv_stride);
-            const int64_t w = sm.w[key];
-            acc[0] += (uint64_t)(w * v.x);
-            acc[1] += (uint64_t)(w * v.y);
-            acc[2] += (uint64_t)(w * v.z);
-            acc[3] += (uint64_t)(w * v.w);
-        }
+        for (uint32_t key = kr; key < tn; key += VAL_RP)
+            weigh_values(acc, sm.w[key], *(const int4*)(vb + (size_t)(t0 + key) * a.kv_stride));
         __syncthreads();
     }
     wpart = (int32_t)wave_sum_u64((uint64_t)(uint32_t)wpart);
-    if (lane == 0) sm.wsum[wave] = wpart;
-#pragma unroll
-    for (int c = 0; c < 4; c++) sm.part[kr * VAL_DS + d4 + c] = (int64_t)acc[c];
-    __syncthreads();
-    if (tid < VAL_DS) {
-        int32_t wsum = 0;
-        for (uint32_t i = 0; i < VAL_NW; i++) wsum = dn::add_sat(wsum, sm.wsum[i]);
-        uint64_t t = 0;
-        for (uint32_t r = 0; r < 64; r++) t += (uint64_t)sm.part[r * VAL_DS + tid];
-        const int64_t resid = dn::sub_sat(dn::ONE_ACT, wsum);
-        t += (uint64_t)(resid * a.v_cache[(size_t)(start + m.i) * a.kv_stride + (size_t)kvh * HD + slice * VAL_DS + tid]);
-        a.ctx[(size_t)head * HD + slice * VAL_DS + tid] = dn::requantize((int64_t)t);
-    }
+    values_finish<HD>(a, sm, acc, wpart, vmax, head, slice);
 }
 
+// Workgroup (head, slice) over `chunks` scores workgroups per head.
 template <uint32_t HD>
-__global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
+__global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a, uint32_t chunks) {
     constexpr uint32_t NT = VAL_NT, NWV = VAL_NW;
-    constexpr uint32_t DS = VAL_DS;                         // dimensions per workgroup
-    constexpr uint32_t VR = 16;                             // 64-key value rounds loaded before the softmax
-    constexpr uint32_t EPT = ATTN_TILE_KEYS / NT;           // keys per thread, at most
+    constexpr uint32_t VR = 1024 / VAL_RP;        // value passes loaded before the softmax (1024 rows)
+    constexpr uint32_t EPT = ATTN_TILE_KEYS / NT;  // keys per thread, at most
     __shared__ ValuesSmem sm;
-    int32_t* s_w = sm.w;
-    int64_t* s_part = sm.part;
-    ArgMax* s_am = sm.am;
-    uint64_t* s_sum = sm.sum;
-    int32_t* s_wsum = sm.wsum;
     const uint2 hs = xcd_head_order(a, blockIdx.x, HD / VAL_DS);
     const uint32_t head = hs.x, slice = hs.y, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t kvh = head / (a.heads / a.kv_heads);
     const uint32_t pos = (uint32_t)(*a.d_pos);
     const uint32_t start = (a.window == 0 || pos + 1 <= a.window) ? 0 : pos + 1 - a.window;
     const uint32_t n = pos - start + 1;
+
+    // 1. The scores workgroups' maxima and this thread's scores (keys
+    // tid + NT*u, increasing), issued by every wave before any wave's value
+    // loads so that they do not queue behind them; then the slice's value
+    // rows. Every load is unconditional (indices past the view clamped to
+    // the first key): a conditional load would be waited for where its
+    // branch joins.
+    uint64_t mk = lane < chunks ? chunk_maxima(a)[(size_t)head * ATTN_DECODE_CHUNKS + lane] : 0;
     if (n > ATTN_TILE_KEYS) {  // uniform over the launch
-        values_long<HD>(a, sm, head, slice, kvh, start, n);
+        values_long<HD>(a, sm, head_first_max(mk), head, slice, kvh, start, n);
         return;
     }
-
-    // 1. This thread's scores (keys tid + NT*u, increasing), then the slice's
-    // value rows; both loads are unconditional (clamped indices), the scores
-    // first so that waiting for them does not wait for the values.
     const int32_t* sb = a.scores + (size_t)head * a.k_pos_stride + start;
     int32_t sc[EPT];
 #pragma unroll
@@ -242,33 +314,24 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
         const uint32_t j = tid + NT * u;
         sc[u] = sb[j < n ? j : 0];
     }
-    const uint32_t kr = tid / 8, d4 = (tid % 8) * 4;
-    const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * HD + slice * DS + d4;
+    asm volatile("s_barrier" ::: "memory");
+    const uint32_t kr = tid / VAL_TPR, d4 = (tid % VAL_TPR) * 4;
+    const int32_t* vb = a.v_cache + (size_t)start * a.kv_stride + (size_t)kvh * HD + slice * VAL_DS + d4;
     int4 vv[VR];
 #pragma unroll
     for (uint32_t r = 0; r < VR; r++) {
-        const uint32_t key = kr + 64 * r;
+        const uint32_t key = kr + VAL_RP * r;
         vv[r] = *(const int4*)(vb + (size_t)(key < n ? key : 0) * a.kv_stride);
     }
+    // Every value load issues before the wait for the maxima: mk passes
+    // through an ordered statement after them.
+    asm volatile("" : "+v"(mk)::"memory");
 
-    // 2. The first maximum, as the largest key (score with its sign bit
-    // flipped, then the complemented index: equal scores favour the lower
-    // index; 0 = no key).
-    uint64_t best = 0;
-#pragma unroll
-    for (uint32_t u = 0; u < EPT; u++) {
-        const uint32_t j = tid + NT * u;
-        const uint64_t k = ((uint64_t)((uint32_t)sc[u] ^ 0x80000000u) << 32) | (uint32_t)~j;
-        best = (j < n) & (k > best) ? k : best;
-    }
-    best = wave_max_u64(best);
-    if (lane == 0) s_am[wave] = ArgMax{(int32_t)((uint32_t)(best >> 32) ^ 0x80000000u), ~(uint32_t)best};
-    lds_barrier();  // the value loads stay in flight
-    ArgMax m = s_am[0];
-    for (uint32_t i = 1; i < NWV; i++) m = argmax_combine(m, s_am[i]);
-
-    // 3. Exp terms (non-negative: their sum is order-free and cannot
-    // saturate for ATTN_TILE_KEYS keys) and 4. the weights and their sum.
+    // 2. The first maximum, in every wave; 3. the exp terms (non-negative:
+    // their sum is order-free and cannot saturate for ATTN_TILE_KEYS keys)
+    // and 4. the weights.
+    const ArgMax m = head_first_max(mk);
+    const int32_t vmax = first_max_value<HD>(a, m, slice, kvh, start);
     uint64_t ev[EPT];
     uint64_t part = 0;
 #pragma unroll
@@ -280,10 +343,11 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
         part += ev[u];
     }
     part = wave_sum_u64(part);
-    if (lane == 0) s_sum[wave] = part;
+    if (lane == 0) sm.sum[wave] = part;
     lds_barrier();
     uint64_t total = 0;
-    for (uint32_t i = 0; i < NWV; i++) total += s_sum[i];
+#pragma unroll
+    for (uint32_t i = 0; i < NWV; i++) total += sm.sum[i];
     const double w_scale = 65536.0 / (double)total, q_scale = 4294967296.0 / (double)total;
     int32_t wpart = 0;
 #pragma unroll
@@ -291,62 +355,36 @@ __global__ __launch_bounds__(512) void attn_values_kernel(const AttnArgs a) {
         const uint32_t j = tid + NT * u;
         if (j < n) {
             const int32_t w = dn::softmax_weight_fast(ev[u], total, w_scale, q_scale);
-            s_w[j] = w;
+            sm.w[j] = w;
             wpart += w;
         }
     }
-    // Weights are non-negative and sum to 2^16 plus at most one half per
-    // key: the saturating sum never saturates, a plain sum is the same.
     wpart = (int32_t)wave_sum_u64((uint64_t)(uint32_t)wpart);
-    if (lane == 0) s_wsum[wave] = wpart;
     lds_barrier();
-    int32_t wsum = 0;
-    for (uint32_t i = 0; i < NWV; i++) wsum = dn::add_sat(wsum, s_wsum[i]);
 
-    // 5. Weighted values of the slice (wrapping i64), 64 key rows in parallel.
-    uint64_t acc[4] = {0, 0, 0, 0};
+    // 5. Weighted values of the slice (wrapping i64), VAL_RP rows per pass.
+    double acc[4] = {0, 0, 0, 0};
 #pragma unroll
     for (uint32_t r = 0; r < VR; r++) {
-        const uint32_t key = kr + 64 * r;
-        if (key < n) {
-            const int64_t w = s_w[key];
-            acc[0] += (uint64_t)(w * vv[r].x);
-            acc[1] += (uint64_t)(w * vv[r].y);
-            acc[2] += (uint64_t)(w * vv[r].z);
-            acc[3] += (uint64_t)(w * vv[r].w);
-        }
+        const uint32_t key = kr + VAL_RP * r;
+        if (key < n) weigh_values(acc, sm.w[key], vv[r]);
     }
-    for (uint32_t key = kr + 64 * VR; key < n; key += 64) {
-        const int4 v = *(const int4*)(vb + (size_t)key * a.kv_stride);
-        const int64_t w = s_w[key];
-        acc[0] += (uint64_t)(w * v.x);
-        acc[1] += (uint64_t)(w * v.y);
-        acc[2] += (uint64_t)(w * v.z);
-        acc[3] += (uint64_t)(w * v.w);
-    }
-#pragma unroll
-    for (int c = 0; c < 4; c++) s_part[kr * DS + d4 + c] = (int64_t)acc[c];
-    lds_barrier();
-    if (tid < DS) {
-        uint64_t t = 0;
-        for (uint32_t r = 0; r < 64; r++) t += (uint64_t)s_part[r * DS + tid];
-        // The first maximum's weight w becomes add_sat(w, ONE - sum): no
-        // saturation for these magnitudes, so the change is + (ONE - sum) * v.
-        const int64_t resid = dn::sub_sat(dn::ONE_ACT, wsum);
-        t += (uint64_t)(resid * a.v_cache[(size_t)(start + m.i) * a.kv_stride + (size_t)kvh * HD + slice * DS + tid]);
-        a.ctx[(size_t)head * HD + slice * DS + tid] = dn::requantize((int64_t)t);
-    }
+    for (uint32_t key = kr + VAL_RP * VR; key < n; key += VAL_RP)
+        weigh_values(acc, sm.w[key], *(const int4*)(vb + (size_t)key * a.kv_stride));
+    values_finish<HD>(a, sm, acc, wpart, vmax, head, slice);
 }
 
 template <uint32_t HD>
 int attention_decode_launch(const AttnArgs& a, hipStream_t stream) {
-    // Up to 32 chunk workgroups per head (longer views loop over chunks),
-    // rounded up so that the KV heads' chunks fill the XCDs evenly (the
-    // extra workgroups find no visible key).
+    // Up to ATTN_DECODE_CHUNKS chunk workgroups per head (longer views loop
+    // over chunks), rounded up so that the KV heads' chunks fill the XCDs
+    // evenly (the extra workgroups find no visible key).
     const uint32_t step = 8 / std::gcd(a.kv_heads, 8u);
-    const uint32_t chunks = (min(a.k_pos_stride / 64, 32u) + step - 1) / step * step;
+    const uint32_t chunks = (min(a.k_pos_stride / 64, ATTN_DECODE_CHUNKS) + step - 1) / step * step;
+    static_assert(ATTN_DECODE_CHUNKS % 8 == 0 && ATTN_DECODE_CHUNKS <= 64, "chunk maxima: one wave's lanes");
+    static_assert(HD % VAL_DS == 0, "whole slices");
     hipLaunchKernelGGL(attn_scores_kernel<HD>, dim3(a.heads * chunks), dim3(256), 0, stream, a, chunks);
-    hipLaunchKernelGGL(attn_values_kernel<HD>, dim3(a.heads * (HD / 32)), dim3(512), 0, stream, a);
+    hipLaunchKernelGGL(attn_values_kernel<HD>, dim3(a.heads * (HD / VAL_DS)), dim3(VAL_NT), 0, stream, a, chunks);
     return (int)hipGetLastError();
 }
 

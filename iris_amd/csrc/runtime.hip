@@ -1052,7 +1052,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     if (st == hipSuccess) st = hipMalloc((void**)&s->ssq_x, GEMV_SSQ_SLOTS * sizeof(int64_t));
     if (st == hipSuccess) st = hipMalloc((void**)&s->ssq_att, GEMV_SSQ_SLOTS * sizeof(int64_t));
     alloc(&s->q, (size_t)max_rows * qw);
-    alloc(&s->scores, (size_t)d.heads * s->k_pos_stride);
+    alloc(&s->scores, attn_scores_ints(d.heads, s->k_pos_stride));
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
     if (max_rows > 1) {

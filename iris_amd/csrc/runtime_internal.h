@@ -77,7 +77,7 @@ struct IrisSession {
     // first row sees before `start`.
     std::vector<uint32_t> kv_lo, kv_hi;
     int32_t *x = nullptr, *attended = nullptr, *q = nullptr, *ctx = nullptr, *gated = nullptr;
-    int32_t* scores = nullptr;  // one-row attention: [heads][k_pos_stride]
+    int32_t* scores = nullptr;  // one-row attention: attn_scores_ints(heads, k_pos_stride)
     // One-row passes: per-tile sums of squares of x and attended, written by
     // the residual products and read by the norms that follow them.
     int64_t *ssq_x = nullptr, *ssq_att = nullptr;
