@@ -111,6 +111,8 @@ extern "C" {
     pub fn iris_memcpy_d2d(dst: *mut c_void, src: *const c_void, bytes: u64) -> c_int;
     pub fn iris_probe_hbm_read(d_buf: *const c_void, bytes: u64, repeats: u32, gb_per_s: *mut f64) -> c_int;
     pub fn iris_probe_mfma_i8(random_operands: u32, iterations: u32, tops: *mut f64) -> c_int;
+    pub fn iris_probe_handoff(workgroups: u32, round_trip_us: *mut f64, atomic_us: *mut f64, barrier_us: *mut f64)
+        -> c_int;
     pub fn iris_time_product(
         matrices: *const *const Q8GpuMatrix,
         count: u32,

@@ -161,6 +161,15 @@ int iris_time_product_ws(const Q8GpuMatrix* matrix, const int32_t* d_activations
  * change every instruction (1). */
 int iris_probe_hbm_read(const void* d_buf, uint64_t bytes, uint32_t repeats, double* gb_per_s);
 int iris_probe_mfma_i8(uint32_t random_operands, uint32_t iterations, double* tops);
+/* Handoffs between workgroups inside one launch (no counterpart in the
+ * reference; what a kernel that waits on other workgroups pays, against a
+ * launch boundary): the round trip of a flag between two workgroups on
+ * different XCDs through agent-scope atomic stores and loads, in
+ * microseconds; one of a chain of dependent agent-scope atomic adds, in
+ * microseconds; and an arrival barrier of `workgroups` (2..1024) workgroups
+ * on one counter, from the last arrival to the last release, in
+ * microseconds. Every wait is bounded: -4 when one gave up. */
+int iris_probe_handoff(uint32_t workgroups, double* round_trip_us, double* atomic_us, double* barrier_us);
 
 /* ------------------------------------------------------------------------
  * The deterministic token loop, device-resident.

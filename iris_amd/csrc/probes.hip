@@ -4,6 +4,7 @@
 // random operands (the matrix cores' clock falls under switching
 // operands, so the second is the ceiling the exact products can meet).
 #include <algorithm>
+#include <vector>
 
 #include "q8_internal.h"
 
@@ -80,6 +81,69 @@ __global__ __launch_bounds__(256) void mfma_i8_kernel(uint32_t rounds, uint32_t*
 #pragma unroll
         for (int e = 0; e < 16; e++) s ^= acc[c][e];
     if ((uint32_t)s == 0x9E3779B9u) out[blockIdx.x] = (uint32_t)s;
+}
+
+// ---- Handoffs between workgroups ----
+// Every wait polls at most HANDOFF_SPIN times (each poll a memory round
+// trip) and then gives up, setting err, so every workgroup ends. Times come
+// from s_memrealtime, a device-wide 100 MHz counter (10 ns per tick).
+constexpr uint32_t HANDOFF_SPIN = 1u << 20;
+
+__device__ __forceinline__ uint32_t poll(uint32_t* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+__device__ __forceinline__ void post(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Workgroups 0 and 1 (dealt to different XCDs) pass a flag back and forth
+// `rounds` times through agent-scope atomic stores and loads: flags[0] from
+// workgroup 0, flags[32] (another cache line) from workgroup 1. out[0..1]:
+// workgroup 0's first and last tick.
+__global__ void handoff_pingpong_kernel(uint32_t* flags, uint64_t* out, uint32_t rounds, uint32_t* err) {
+    if (threadIdx.x != 0) return;
+    const bool first = blockIdx.x == 0;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t r = 1; r <= rounds; r++) {
+        if (first) post(&flags[0], r);
+        uint32_t n = 0;
+        while (poll(&flags[first ? 32 : 0]) != r)
+            if (++n == HANDOFF_SPIN) break;
+        if (n == HANDOFF_SPIN) {
+            post(err, 1);
+            break;
+        }
+        if (!first) post(&flags[32], r);
+    }
+    if (first) {
+        out[0] = t0;
+        out[1] = __builtin_amdgcn_s_memrealtime();
+    }
+}
+
+// `count` dependent agent-scope atomic adds on one word; out[0]: the ticks.
+__global__ void handoff_atomic_chain_kernel(uint32_t* word, uint64_t* out, uint32_t count) {
+    if (threadIdx.x != 0) return;
+    uint32_t v = 0;
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    for (uint32_t i = 0; i < count; i++)
+        v = __hip_atomic_fetch_add(word + (v >> 31), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    out[0] = __builtin_amdgcn_s_memrealtime() - t0;
+    out[1] = v;
+}
+
+// Every workgroup adds one to *count and polls it until all have: out[2g]
+// its arrival tick, out[2g + 1] its release tick.
+__global__ void handoff_barrier_kernel(uint32_t* count, uint64_t* out, uint32_t* err) {
+    if (threadIdx.x != 0) return;
+    const uint64_t ta = __builtin_amdgcn_s_memrealtime();
+    __hip_atomic_fetch_add(count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t n = 0;
+    while (poll(count) < gridDim.x)
+        if (++n == HANDOFF_SPIN) {
+            post(err, 1);
+            break;
+        }
+    out[2 * blockIdx.x] = ta;
+    out[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
 }
 
 template <class Launch>
@@ -160,4 +224,47 @@ extern "C" int iris_probe_mfma_i8(uint32_t random_operands, uint32_t iterations,
         *tops = ops / (ms * 1e-3) / 1e12;
     }
     return rc;
+}
+
+extern "C" int iris_probe_handoff(uint32_t workgroups, double* round_trip_us, double* atomic_us, double* barrier_us) {
+    if (!round_trip_us || !atomic_us || !barrier_us || workgroups < 2 || workgroups > 1024) return IRIS_E_INVALID;
+    constexpr uint32_t ROUNDS = 2000, CHAIN = 1000;
+    // [0, 256): flags and counters; then err; then the barrier's ticks.
+    uint32_t* mem = nullptr;
+    hipError_t st = hipMalloc((void**)&mem, 4096 + 16ull * workgroups);
+    if (st != hipSuccess) return (int)st;
+    uint32_t* err = mem + 256;
+    uint64_t* ticks = (uint64_t*)(mem + 512);
+    std::vector<uint64_t> h(2 * (size_t)workgroups);
+    uint32_t herr = 0;
+    auto run = [&](auto launch, size_t n_ticks) -> hipError_t {
+        hipError_t e = hipMemset(mem, 0, 4096);
+        if (e == hipSuccess) {
+            launch();
+            e = hipGetLastError();
+        }
+        if (e == hipSuccess) e = hipDeviceSynchronize();
+        if (e == hipSuccess) e = hipMemcpy(h.data(), ticks, n_ticks * 8, hipMemcpyDeviceToHost);
+        if (e == hipSuccess) e = hipMemcpy(&herr, err, 4, hipMemcpyDeviceToHost);
+        return e;
+    };
+    st = run([&] { hipLaunchKernelGGL(handoff_pingpong_kernel, dim3(2), dim3(64), 0, nullptr, mem, ticks, ROUNDS, err); }, 2);
+    if (st == hipSuccess && !herr) *round_trip_us = (double)(h[1] - h[0]) * 0.01 / ROUNDS;
+    if (st == hipSuccess && !herr)
+        st = run([&] { hipLaunchKernelGGL(handoff_atomic_chain_kernel, dim3(1), dim3(64), 0, nullptr, mem, ticks, CHAIN); }, 2);
+    if (st == hipSuccess && !herr) *atomic_us = (double)h[0] * 0.01 / CHAIN;
+    if (st == hipSuccess && !herr)
+        st = run([&] { hipLaunchKernelGGL(handoff_barrier_kernel, dim3(workgroups), dim3(64), 0, nullptr, mem, ticks, err); },
+                 2 * (size_t)workgroups);
+    if (st == hipSuccess && !herr) {
+        uint64_t last_arrival = 0, last_release = 0;
+        for (uint32_t g = 0; g < workgroups; g++) {
+            last_arrival = std::max(last_arrival, h[2 * g]);
+            last_release = std::max(last_release, h[2 * g + 1]);
+        }
+        *barrier_us = (double)(last_release - last_arrival) * 0.01;
+    }
+    hipFree(mem);
+    if (st != hipSuccess) return (int)st;
+    return herr ? IRIS_E_STATE : 0;
 }

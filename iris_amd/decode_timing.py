@@ -359,6 +359,22 @@ def measured_peaks(stream_bytes: int = 1 << 30) -> dict:
     return out
 
 
+def handoff_latencies(sizes=(8, 32, 288, 1024)) -> dict:
+    """What a kernel pays to wait on other workgroups, against a launch
+    boundary: a flag's round trip between workgroups on two XCDs, one
+    dependent agent-scope atomic add, and arrival barriers of `sizes`
+    workgroups on one counter (last arrival to last release)."""
+    L = native.lib()
+    out = {}
+    for g in sizes:
+        rt, at, bar = C.c_double(), C.c_double(), C.c_double()
+        native.check(L.iris_probe_handoff(g, C.byref(rt), C.byref(at), C.byref(bar)), "handoff probe")
+        out["flag_round_trip_us"] = round(rt.value, 3)
+        out["atomic_add_us"] = round(at.value, 3)
+        out[f"barrier_{g}_workgroups_us"] = round(bar.value, 2)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
     ap.add_argument("--steps", type=int, default=PROMPT - 1)
@@ -382,7 +398,8 @@ def main(argv=None):
                          "counters); Mistral-7B shape, or Gemma-2B shape with --gemma")
     ap.add_argument("--gemma", action="store_true", help="with --eager-decode: the Gemma-2B shape")
     ap.add_argument("--peaks", action="store_true",
-                    help="only the measured peaks: HBM read stream and int8 MFMA (constant and random operands)")
+                    help="only the measured peaks: HBM read stream and int8 MFMA (constant and random operands), "
+                         "and the handoff latencies between workgroups")
     args = ap.parse_args(argv)
     global USE_GRAPH
     if USE_GRAPH and native.kernel_tracer_loaded():
@@ -392,6 +409,7 @@ def main(argv=None):
     native.check(native.lib().q8gpu_init(), "q8gpu_init")
     if args.peaks:
         print(json.dumps(measured_peaks()), flush=True)
+        print(json.dumps(handoff_latencies()), flush=True)
         return
     if args.eager_decode:
         print(json.dumps(eager_decode(args.eager_decode, args.gemma)), flush=True)
