@@ -88,13 +88,14 @@ int q8gpu_product_device_ws(const Q8GpuMatrix* matrix, const int32_t* d_activati
 
 /* Folds a per-block scale matrix's scales into weight digit planes so that
  * its multi-token products (q8gpu_product_device_ws, _noalloc and
- * q8gpu_product) run on the int8 matrix cores. Allocates up to
- * Q8_FOLD_MAX_PLANES (4) x rows x cols bytes more device memory (reported by
- * q8gpu_matrix_info's bytes) and synchronises `stream`. Does nothing, and
- * returns 0, for a row-scale matrix, one already prepared, or one whose
- * scales spread over too many binary orders (its products stay on the
- * vector path, same bits). Not to be called while other calls use the
- * matrix. No counterpart in the reference (whose device cache budgets
+ * q8gpu_product) run on the int8 matrix cores. Every matrix of finite
+ * scales folds: 1 to Q8_FOLD_MAX_PLANES (6) planes, by how far a row's
+ * scales spread (3 for the reference bundles' layout, 6 for a subnormal
+ * block beside exponent 30). Allocates that many x rows x cols bytes more
+ * device memory, plus 4 bytes per row (reported by q8gpu_matrix_info's
+ * bytes), and synchronises `stream`. Does nothing, and returns 0, for a
+ * row-scale matrix or one already prepared. Not to be called while other
+ * calls use the matrix. No counterpart in the reference (whose device cache budgets
  * rows*cols + blocks*8 bytes per matrix, gpu.rs:171-173: a prepared matrix
  * holds more). */
 int q8gpu_prepare_matrix_cores(Q8GpuMatrix* matrix, void* stream);

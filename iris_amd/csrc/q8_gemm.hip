@@ -502,13 +502,22 @@ __global__ __launch_bounds__(64 * W * SPLIT, 1) void q8_gemm_row_kernel(const Ge
 // (crates/det-num/src/q8.rs:56-72). Each w' is split into WP signed byte
 // digits like the activations, so every (weight digit p, activation digit
 // l) pair is an int8 GEMM with exact int32 sums, and pairs with the same
-// p + l share an accumulator (at most four terms of |.| <= K * 2^14 each,
-// below 2^31 for K <= 16384). The epilogue recombines the shifts in 128
+// p + l share an accumulator (at most five terms of |.| <= K * 2^14 each:
+// 5 * 2^28 < 2^31 for K <= 16384). The epilogue recombines the shifts in 128
 // bits, shifts by R and rounds once at 24 fraction bits.
+
+// The signed byte digits of |v| < 2^47 (six bytes, d_l = byte l as int8,
+// v = sum_l 256^l d_l) and how many of them v needs.
+__device__ __forceinline__ uint64_t digits6(int64_t v) {
+    return (uint64_t)(v + 0x808080808080LL) ^ 0x808080808080ULL;
+}
+__device__ __forceinline__ int digits6_needed(uint64_t d) {
+    return (d >> 40) ? 6 : (d >> 32) ? 5 : (d >> 24) ? 4 : (d >> 16) ? 3 : (d >> 8) ? 2 : 1;
+}
 
 // Per row: R (the least exponent shift of its non-zero block scales; 0 for
 // an all-zero row) into shift[row], and the digits its largest |w'| needs
-// raised into *need (more than Q8_FOLD_MAX_PLANES: the row cannot fold).
+// raised into *need (at most 6: sh_b - R <= 29, so |w'| < 2^47).
 __global__ __launch_bounds__(256) void fold_rows_kernel(const uint8_t* qs, const uint16_t* sc16, uint32_t rows,
                                                         uint32_t nb, int32_t* shift, int* need) {
     const uint32_t row = blockIdx.x * blockDim.x + threadIdx.x;
@@ -529,11 +538,7 @@ __global__ __launch_bounds__(256) void fold_rows_kernel(const uint8_t* qs, const
         const uint32_t bits = sc[(size_t)b * Q8_TILE_ROWS], e = (bits >> 10) & 0x1f, mant = bits & 0x3ff;
         const int64_t m = (int64_t)(e ? 1024 + mant : mant);
         if (m == 0) continue;
-        const int d = (e ? (int)e - 1 : 0) - least;
-        if (d > 20) {
-            digits = 5;
-            break;
-        }
+        const int d = (e ? (int)e - 1 : 0) - least;  // 0..29
         // The largest |q| of the block (both signs: digits are asymmetric).
         int qmax = 0, qmin = 0;
         const uint8_t* qb = q + (size_t)b * Q8_TILE_BLOCK_BYTES;
@@ -544,11 +549,7 @@ __global__ __launch_bounds__(256) void fold_rows_kernel(const uint8_t* qs, const
                 qmin = min(qmin, v);
             }
         const int64_t f = (bits & 0x8000) ? -(m << d) : (m << d);
-        for (int64_t wv : {f * qmax, f * qmin}) {
-            const uint64_t dg = (uint64_t)(wv + 0x8080808080LL) ^ 0x8080808080ULL;
-            const int n = (dg >> 32) ? 5 : (dg >> 24) ? 4 : (dg >> 16) ? 3 : (dg >> 8) ? 2 : 1;
-            digits = max(digits, n);
-        }
+        for (int64_t wv : {f * qmax, f * qmin}) digits = max(digits, digits6_needed(digits6(wv)));
     }
     atomicMax(need, digits);
 }
@@ -576,8 +577,7 @@ __global__ __launch_bounds__(256) void fold_planes_kernel(const uint8_t* qs, con
         for (int c = 0; c < 4; c++) {
             uint64_t dg[4];
 #pragma unroll
-            for (int k = 0; k < 4; k++)
-                dg[k] = (uint64_t)((int64_t)(int8_t)(qw[c] >> (8 * k)) * f + 0x8080808080LL) ^ 0x8080808080ULL;
+            for (int k = 0; k < 4; k++) dg[k] = digits6((int64_t)(int8_t)(qw[c] >> (8 * k)) * f);
 #pragma unroll
             for (uint32_t p = 0; p < Q8_FOLD_MAX_PLANES; p++) out[p][c] = plane_byte4(dg[0], dg[1], dg[2], dg[3], p);
         }
@@ -593,8 +593,8 @@ __global__ __launch_bounds__(256) void fold_planes_kernel(const uint8_t* qs, con
 // planes and LG activation planes.
 template <int WP, int LG>
 struct FoldShape {
-    // Two row tiles per wave up to three weight planes; one for four (whose
-    // accumulators would not fit twice).
+    // Two row tiles per wave up to three weight planes; one for four to six
+    // (whose accumulators would not fit twice).
     static constexpr int RI = WP <= 3 ? 2 : 1;
     static constexpr uint32_t WAVES = 4, THREADS = 256, RT = 2 * RI;
     static constexpr uint32_t CHUNKS = 2 * RT * WP + 2 * LG * 2;
@@ -699,7 +699,7 @@ __device__ __forceinline__ void fold_pass(const GemvArgs& a, int8_t* smem, uint3
     });
 }
 
-// 128 folded weight rows (64 for four planes) x 64 tokens per workgroup, blocks ordered as in
+// 128 folded weight rows (64 for four to six planes) x 64 tokens per workgroup, blocks ordered as in
 // q8_gemm_row_kernel (contiguous ranges per XCD, bands of 8 row groups).
 template <int WP>
 __global__ __launch_bounds__(256, 1) void q8_gemm_fold_kernel(const GemvArgs a) {
@@ -750,14 +750,16 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return (int)st;
     if (a.w.scale_mode == Q8_SCALE_F16) {
-        // 32-row tiles per workgroup: 4, or 2 for four planes (FoldShape::RT).
+        // 32-row tiles per workgroup: 4, or 2 for four to six planes (FoldShape::RT).
         const uint32_t rt = a.w.fold_nplanes <= 3 ? 4 : 2;
         const uint32_t n = (a.w.tiles + 2 * rt - 1) / (2 * rt) * ((TT + 1) / 2);
         switch (a.w.fold_nplanes) {
             case 1: hipLaunchKernelGGL(q8_gemm_fold_kernel<1>, dim3(n), dim3(256), 0, stream, a); break;
             case 2: hipLaunchKernelGGL(q8_gemm_fold_kernel<2>, dim3(n), dim3(256), 0, stream, a); break;
             case 3: hipLaunchKernelGGL(q8_gemm_fold_kernel<3>, dim3(n), dim3(256), 0, stream, a); break;
-            default: hipLaunchKernelGGL(q8_gemm_fold_kernel<4>, dim3(n), dim3(256), 0, stream, a); break;
+            case 4: hipLaunchKernelGGL(q8_gemm_fold_kernel<4>, dim3(n), dim3(256), 0, stream, a); break;
+            case 5: hipLaunchKernelGGL(q8_gemm_fold_kernel<5>, dim3(n), dim3(256), 0, stream, a); break;
+            default: hipLaunchKernelGGL(q8_gemm_fold_kernel<6>, dim3(n), dim3(256), 0, stream, a); break;
         }
         return (int)hipGetLastError();
     }

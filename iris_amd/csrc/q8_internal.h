@@ -40,10 +40,14 @@ constexpr int Q8_TILE_BLOCK_BYTES = 512;
 struct Q8Folded {
     int8_t* planes;    // [planes][tiles][nb][512]
     int32_t* shift;    // [tiles * 16]
-    uint32_t nplanes;  // 0 = not prepared (or the spread of a row's scales is too wide)
+    uint32_t nplanes;  // 0 = not prepared
 };
 
-constexpr uint32_t Q8_FOLD_MAX_PLANES = 4;
+// Weight digit planes of a folded matrix, at most: the widest spread of a
+// row's f16 scales (a subnormal block beside exponent 30, 29 binary orders)
+// makes |w'| <= 127 * 2047 * 2^29 < 2^47, six signed byte digits, so every
+// matrix with finite scales folds.
+constexpr uint32_t Q8_FOLD_MAX_PLANES = 6;
 
 struct Q8GpuMatrix {
     uint32_t rows, cols, nb, tiles;
@@ -77,8 +81,7 @@ inline Q8View q8_view(const Q8GpuMatrix* m) {
 
 // Builds m's folded planes (once; per-block scale matrices only) so that
 // multi-token products of it run on the matrix cores. Allocates device
-// memory. Leaves m unfolded, and returns 0, when a row's scales spread over
-// too many binary orders for Q8_FOLD_MAX_PLANES digits.
+// memory (one byte per weight per digit plane, 1 to Q8_FOLD_MAX_PLANES).
 int iris_q8_prepare_fold(Q8GpuMatrix* m, hipStream_t stream);
 
 // Prologue applied to the activations while they are staged.

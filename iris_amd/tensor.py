@@ -53,9 +53,9 @@ class Q8Matrix:
         return self._h
 
     def prepare_matrix_cores(self):
-        """Fold a per-block scale matrix for the int8 matrix cores (more
-        device memory; nothing for a row-scale matrix or a too-wide spread):
-        its multi-token products then run there."""
+        """Fold a per-block scale matrix for the int8 matrix cores (one to
+        six more bytes per weight, by how far a row's scales spread; nothing
+        for a row-scale matrix): its multi-token products then run there."""
         native.check(native.lib().q8gpu_prepare_matrix_cores(self._h, None), "prepare matrix cores")
 
     def info(self):

@@ -260,14 +260,21 @@ def per_block_matrix(rng, rows, cols, kind):
     byte: `kind` sets how the scales of a row spread (so how many digit
     planes the folded weights need): "tiny" subnormal scales below 2^-17
     (one or two planes), "same" one exponent per row with random
-    significands (three), "unit" scales of 0 or 2^-24 (one plane),
+    significands (three), "unit" scales of 0 or 2^-24 (one plane, or two
+    where a negative scale meets q = -128: w' = 128),
     "spread4" exponents within 4 binary orders
-    (three), "spread12" within 12 (four), "wide" over 20 orders (not
-    foldable: the vector path), "top" exponents 26..30 (results saturate),
-    plus zero scales and all-zero rows."""
+    (three), "spread12" within 12 (four), "wide" over 20 orders (five),
+    "widest" every exponent 0..30 with subnormals beside the largest
+    scales (six: the widest spread an f16 scale row can have), "top"
+    exponents 26..30 (results saturate), plus zero scales and all-zero
+    rows."""
     nb = cols // 32
     base = rng.integers(1, 17, (rows, 1))
-    if kind == "tiny":
+    if kind == "widest":
+        e = rng.integers(0, 31, (rows, nb))
+        e[:, 0], e[:, -1] = 0, 30  # a subnormal block and an exponent-30 block in every row
+        mant = rng.integers(1, 1024, (rows, nb))
+    elif kind == "tiny":
         e = np.zeros((rows, nb), np.int64)
         mant = rng.integers(0, 96, (rows, nb))
     elif kind == "unit":
@@ -288,15 +295,15 @@ def per_block_matrix(rng, rows, cols, kind):
     return raw.reshape(rows, -1)
 
 
-@pytest.mark.parametrize("kind,folds", [("unit", True), ("tiny", True), ("same", True), ("spread4", True),
-                                        ("spread12", True), ("wide", False), ("top", True)])
+@pytest.mark.parametrize("kind,planes", [("unit", None), ("tiny", None), ("same", 3), ("spread4", 3),
+                                         ("spread12", 4), ("wide", 5), ("widest", 6), ("top", 3)])
 @pytest.mark.parametrize("tokens,rows,cols", [(603, 200, 128), (129, 136, 4160)])
-def test_per_block_scales_on_the_matrix_cores(kind, folds, tokens, rows, cols):
+def test_per_block_scales_on_the_matrix_cores(kind, planes, tokens, rows, cols):
     # Per-block scale matrices folded into weight digit planes for the int8
-    # matrix cores (or, when a row's scales spread too wide, left to the
-    # vector path): every digit count of the activations (token groups of
+    # matrix cores, one to six planes (every spread an f16 scale row can
+    # have folds): every digit count of the activations (token groups of
     # 1..5 digits), partial row and token tiles, every output against the
-    # oracle's dot_row.
+    # oracle's dot_row. (None: the count depends on the draw.)
     rng = np.random.default_rng(tokens + rows + len(kind))
     raw = per_block_matrix(rng, rows, cols, kind)
     m = Q8Matrix.from_bytes(raw, rows, cols)
@@ -308,7 +315,13 @@ def test_per_block_scales_on_the_matrix_cores(kind, folds, tokens, rows, cols):
     assert np.array_equal(product_ws(m, x), want)
     assert m.info()["bytes"] == before
     m.prepare_matrix_cores()
-    assert (m.info()["bytes"] > before) == folds  # the folded planes were built
+    # The folded planes were built: one byte per weight per plane (rows
+    # padded to whole 16-row tiles), plus one 32-bit shift per row.
+    tiles = (rows + 15) // 16
+    extra = m.info()["bytes"] - before - tiles * 16 * 4
+    assert extra > 0 and extra % (tiles * 16 * cols) == 0
+    if planes is not None:
+        assert extra // (tiles * 16 * cols) == planes
     got = product_ws(m, x)
     assert np.array_equal(got, want)
     # again, from the folded planes already there
