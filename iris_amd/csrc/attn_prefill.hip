@@ -436,8 +436,9 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
             }
         }
     };
-    // Head size 256: four passes of four d-tiles (two of eight spill).
-    constexpr uint32_t VPASS = HD >= 256 ? 4 : DT;
+    // Head size 256: four passes of four d-tiles (two of eight spill);
+    // 512 (one wave per SIMD): four passes of eight.
+    constexpr uint32_t VPASS = HD >= 512 ? 8 : HD >= 256 ? 4 : DT;
     auto passes = [&](auto self, auto pc) __attribute__((always_inline)) {
         constexpr uint32_t P = decltype(pc)::value;
         values_pass(std::integral_constant<uint32_t, P * VPASS>{}, std::integral_constant<uint32_t, VPASS>{});
@@ -448,9 +449,10 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
 
 // Workgroup: query heads h0..h0+3 (four consecutive heads, one wave each,
 // each with its own KV head) over one 16-row query tile, the longest rows
-// first.
+// first. Two waves per SIMD up to head size 256; one at 512, whose query and
+// key-tile fragments (LQK x 8 each) take 256 registers together.
 template <uint32_t HD>
-__global__ __launch_bounds__(256, 2) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
+__global__ __launch_bounds__(256, HD >= 512 ? 1 : 2) void attn_prefill_kernel(const AttnArgs a, uint32_t tokens) {
     __shared__ union {
         AttnRowSmem row;
         PrefillSmem pre;
@@ -527,10 +529,12 @@ bool iris_attention_prefill_applies(const AttnArgs& a, uint32_t tokens, uint32_t
     const AttnPlanes& p = a.planes;
     // Head size 256 (four value passes) pays off from about 128 workgroups
     // (Gemma-2B shape: 93 against 117 ms for a 2048-row pass, 15.2 against
-    // 12.8 ms for 128 rows on the one-row routine).
-    if (a.head_dim == 256 && (tokens + 15) / 16 * (a.heads / 4) < 128) return false;
+    // 12.8 ms for 128 rows on the one-row routine), and so does 512 (one
+    // wave per SIMD; the scaled gemma-4 shape: 12.5 against 16.7 ms for 2048
+    // rows, 5.2 against 4.9 ms for 600).
+    if (a.head_dim >= 256 && (tokens + 15) / 16 * (a.heads / 4) < 128) return false;
     return tokens >= 2 && p.q && p.k && p.v && p.q_limbs && p.kv_limbs && p.e_store &&
-           (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256) &&
+           (a.head_dim == 64 || a.head_dim == 128 || a.head_dim == 256 || a.head_dim == 512) &&
            a.heads % a.kv_heads == 0 && a.heads % 4 == 0 && (tokens + 15) / 16 <= p.qt_cap &&
            max_keys <= p.ks_cap * 64 && max_keys <= ATTN_MAX_KEYS;
 }
@@ -540,6 +544,7 @@ int iris_attention_prefill_launch(const AttnArgs& a, uint32_t tokens, uint32_t m
     switch (a.head_dim) {
         case 64: return prefill_launch<64>(a, tokens, stream);
         case 128: return prefill_launch<128>(a, tokens, stream);
-        default: return prefill_launch<256>(a, tokens, stream);
+        case 256: return prefill_launch<256>(a, tokens, stream);
+        default: return prefill_launch<512>(a, tokens, stream);
     }
 }

@@ -77,8 +77,8 @@ struct AttnArgs {
 // last row (checked against the kernel's capacity).
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
 // The multi-row MFMA attention (attn_prefill.hip): applies to head sizes 64,
-// 128 and 256 (the last from 128 workgroups on) with a multiple of four
-// query heads, given plane space for `tokens` rows and `max_keys` keys.
+// 128, 256 and 512 (the last two from 128 workgroups on) with a multiple of
+// four query heads, given plane space for `tokens` rows and `max_keys` keys.
 bool iris_attention_prefill_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys);
 int iris_attention_prefill_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
 // *d_pos = pos and *d_step = step, in stream order.

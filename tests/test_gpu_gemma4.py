@@ -69,6 +69,23 @@ def test_teacher_forced_pass_and_ranges(model, oracle_pass):
     s.free()
 
 
+def test_long_pass_on_the_matrix_cores(model):
+    # 1024 rows: 128 workgroups of 16 rows x 4 heads, from which the multi-row
+    # attention runs on the matrix cores for head sizes 256 and 512 (the 600
+    # rows above take the one-row routine). Every layer's rows against the
+    # oracle, the sliding layers' 512-key window in use.
+    m, dm = model
+    n = 1024
+    ids = list(synth.token_ids(0x1024, n, m.vocab))
+    print(f"gemma-4 layout: {n}-row pass on the matrix cores", flush=True)
+    _, layers = cpu.OracleRun(m, n).pass_rows(ids, 0, keep_layers=True)
+    s = Session(dm, n, n)
+    rows, _ = s.layer_pass(ids)
+    for layer in range(m.num_layers):
+        assert np.array_equal(rows[layer], layers[layer]), f"layer {layer} (head size {m.head_dim_at(layer)})"
+    s.free()
+
+
 @pytest.mark.parametrize("use_graph", [True, False])
 def test_generation_every_logit(model, oracle_pass, use_graph):
     m, dm = model
