@@ -122,6 +122,14 @@ extern "C" {
         iterations: u32,
         ms_per_product: *mut f64,
     ) -> c_int;
+    pub fn iris_time_bcast_product(
+        matrices: *const *const Q8GpuMatrix,
+        count: u32,
+        d_activations: *const i32,
+        d_out: *mut i32,
+        iterations: u32,
+        ms_per_product: *mut f64,
+    ) -> c_int;
     pub fn iris_time_product_ws(
         matrix: *const Q8GpuMatrix,
         d_activations: *const i32,

@@ -144,6 +144,17 @@ int iris_memcpy_d2d(void* dst, const void* src, uint64_t bytes);
 int iris_time_product(const Q8GpuMatrix* const* matrices, uint32_t count, const int32_t* d_activations,
                       uint32_t tokens, int32_t* d_out, uint32_t iterations, double* ms_per_product);
 
+/* The one-token product as the decode loop runs it when the row's producer
+ * leaves the row as digit planes (no counterpart in the reference; a
+ * measurement and parity entry): forms the planes of d_activations (one row
+ * of cols int32 values) once, then runs the product from them `iterations`
+ * times back to back cycling through `count` row-scale matrices of one shape
+ * (cols >= 256), as iris_time_product does, and reports the mean time per
+ * product. d_out holds the last product's rows (the same as
+ * q8gpu_product_device's for that matrix). */
+int iris_time_bcast_product(const Q8GpuMatrix* const* matrices, uint32_t count, const int32_t* d_activations,
+                            int32_t* d_out, uint32_t iterations, double* ms_per_product);
+
 /* As iris_time_product for one matrix through q8gpu_product_device_ws: with
  * the work space, multi-token products of row-scale matrices run on the int8
  * matrix cores (digit planes plus the MFMA GEMM), and this times them. */

@@ -70,12 +70,20 @@ struct AttnArgs {
     // kernel), sized by attn_q_planes_bytes / attn_kv_planes_bytes /
     // attn_e_store_bytes.
     AttnPlanes planes;
+    // One-row launches (iris_attention_decode_applies): the context row's
+    // digit planes too, in the act_planes layout over heads*head_dim values
+    // (null: not written).
+    uint32_t* ctx_planes;
+    uint8_t* ctx_counts;
 };
 
 
 // Attention for `tokens` query rows; max_keys bounds the visible keys of the
 // last row (checked against the kernel's capacity).
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream);
+// One row through the two decode launches (chunked scores, then values per
+// 32-dimension slice): the only path that writes ctx_planes.
+bool iris_attention_decode_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys);
 // The multi-row MFMA attention (attn_prefill.hip): applies to head sizes 64,
 // 128, 256 and 512 (the last two from 128 workgroups on) with a multiple of
 // four query heads, given plane space for `tokens` rows and `max_keys` keys.

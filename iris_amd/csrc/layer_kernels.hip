@@ -5,6 +5,7 @@
 #include <numeric>
 #include <mutex>
 
+#include "act_planes.h"
 #include "attn_common.h"
 #include "detnum_dev.h"
 #include "layer_kernels.h"
@@ -224,6 +225,7 @@ __device__ __forceinline__ void values_finish(const AttnArgs& a, ValuesSmem& sm,
         for (int c = 0; c < 4; c++) sm.part[wave][lane * 4 + c] = (int64_t)acc[c];
     if (lane == 0) sm.wsum[wave] = wpart;
     lds_barrier();
+    int32_t out = 0;
     if (tid < VAL_DS) {
         // Weights are non-negative and sum to 2^16 plus at most one half per
         // key: the saturating sum never saturates, a plain sum is the same.
@@ -236,8 +238,13 @@ __device__ __forceinline__ void values_finish(const AttnArgs& a, ValuesSmem& sm,
         }
         const int64_t resid = dn::sub_sat(dn::ONE_ACT, wsum);
         t += (uint64_t)(resid * vmax);
-        a.ctx[(size_t)head * HD + slice * VAL_DS + tid] = dn::requantize((int64_t)t);
+        out = dn::requantize((int64_t)t);
+        a.ctx[(size_t)head * HD + slice * VAL_DS + tid] = out;
     }
+    // The slice is one 32-value block of the context row: its digit planes
+    // for the O product, from wave 0 (threads 0..31 hold the values).
+    if (a.ctx_planes && wave == 0)
+        act_planes_store32(out, lane, head * HD + slice * VAL_DS, a.heads * HD, a.ctx_planes, a.ctx_counts);
 }
 
 // The values workgroup for a view longer than ATTN_TILE_KEYS: the exp sum
@@ -509,10 +516,19 @@ int iris_rope_table_launch(const int64_t* inv_freq, uint32_t half, const int32_t
     return (int)hipGetLastError();
 }
 
+bool iris_attention_decode_applies(const AttnArgs& a, uint32_t tokens, uint32_t max_keys) {
+    const uint32_t hd = a.head_dim;
+    return tokens == 1 && a.scores && a.k_pos_stride % 64 == 0 && max_keys <= a.k_pos_stride &&
+           (hd == 32 || hd == 64 || hd == 128 || hd == 256 || hd == 512);
+}
+
 int iris_attention_launch(const AttnArgs& a, uint32_t tokens, uint32_t max_keys, hipStream_t stream) {
     if (a.head_dim > ATTN_MAX_HEAD_DIM || a.head_dim % 4 || max_keys > ATTN_MAX_KEYS || a.heads % a.kv_heads)
         return IRIS_E_INVALID;
-    if (tokens == 1 && a.scores && a.k_pos_stride % 64 == 0 && max_keys <= a.k_pos_stride) {
+    if ((a.ctx_planes || a.ctx_counts) && !(iris_attention_decode_applies(a, tokens, max_keys) && a.ctx_planes &&
+                                            a.ctx_counts))
+        return IRIS_E_INVALID;
+    if (iris_attention_decode_applies(a, tokens, max_keys)) {
         // One row: the chunked scores, then HD/32 workgroups per head.
         switch (a.head_dim) {
             case 32: return attention_decode_launch<32>(a, stream);

@@ -14,6 +14,7 @@
 // the exact 64-bit block sum.
 #include "detnum_dev.h"
 #include "q8_internal.h"
+#include "act_planes.h"
 #include "q8_epilogue.h"
 #include "wave_ops.h"
 
@@ -245,6 +246,20 @@ __device__ __forceinline__ void finish_tile(const GemvArgs& a, uint32_t tile, ui
         const int32_t o = a.epilogue == EPI_RESIDUAL ? dn::add_sat(v, in.epi.res) : v;
         const int64_t sq = row16_sum_sat_nonneg(own ? (int64_t)o * o : 0);
         if (lane == 0) a.ssq_out[tile] = sq;
+    }
+    if (a.out_planes) {
+        // One gated row (EPI_SWIGLU / EPI_GEGLU, one token): each even lane's
+        // output stored, and the tile's eight outputs as digit planes for the
+        // product that reads them.
+        const bool own = lane < Q8_TILE_ROWS && (lane & 1) == 0 && row < w.rows;
+        int32_t o = 0;
+        if (own) {
+            const int32_t act = a.epilogue == EPI_SWIGLU ? dn::silu(v) : dn::gelu(v);
+            o = dn::mul_sat(act, partner);
+            a.out[row >> 1] = o;
+        }
+        act_planes_store8_even(o, lane, tile * (Q8_TILE_ROWS / 2), w.rows / 2, a.out_planes, a.out_counts);
+        return;
     }
     if (lane >= Q8_TILE_ROWS || row >= w.rows) return;
     store_output_in(a, row, token, v, partner, in.epi);
@@ -986,6 +1001,12 @@ int iris_select_launch(const GemvArgs& a, hipStream_t stream) {
 
 int iris_gemv_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.tokens == 0 || a.w.rows == 0) return 0;
+    if (iris_gemv_bcast_applies(a)) return iris_gemv_bcast_launch(a, stream);
+    // (Planes given where the broadcast product does not apply, e.g. a
+    // per-block scale matrix: the row is staged from x as usual.)
+    if (a.out_planes && (a.tokens != 1 || !a.out_counts || (a.epilogue != EPI_SWIGLU && a.epilogue != EPI_GEGLU) ||
+                         a.w.rows % 64))
+        return IRIS_E_INVALID;
     if (iris_gemm_applies(a)) return iris_gemm_launch(a, stream);
     if (a.w.cols % 32 || a.x_stride % 4 || ((uintptr_t)a.x & 15)) return IRIS_E_INVALID;
     if (a.prologue < PRO_NONE || a.prologue > PRO_NORM_RES_NORM) return IRIS_E_INVALID;

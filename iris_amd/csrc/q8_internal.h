@@ -169,7 +169,36 @@ struct GemvArgs {
     // EPI_SWIGLU of the matrix-core products: the device's silu table
     // (iris_silu_table); null computes each silu.
     const int32_t* silu_tab;
+    // One-token products whose input row comes as digit planes written by
+    // its producer (ActPlanes layout; PRO_NONE, row scales, EPI_RESIDUAL or
+    // EPI_STORE): the row's planes and digit counts, and the k split's
+    // scratch, partial sums [BCAST_MAX_PARTS][rows] and arrival counters
+    // [bcast_groups(rows)] (zero at allocation; each launch leaves them
+    // zero). Null x_planes: the row is staged from x.
+    const uint32_t* x_planes;
+    const uint8_t* x_counts;
+    int64_t* kpart;
+    uint32_t* kcount;
+    // One-token EPI_SWIGLU / EPI_GEGLU launches: the outputs' digit planes
+    // too (ActPlanes layout over out's row; null: not written).
+    uint32_t* out_planes;
+    uint8_t* out_counts;
 };
+
+// A row of int32 values as the broadcast products read it: plane l (of
+// ACT_PLANES) holds dword i = the signed byte digits l of values 4i..4i+3
+// (balanced base 256, digits5), at planes[l * cols/4 + i]; counts[j] holds
+// the digits values 8j..8j+7 need (1-5), so a 32-value block's four counts
+// are one dword. cols % 32 == 0.
+constexpr uint32_t ACT_PLANES = 5;  // signed byte digits of an int32
+inline uint64_t act_planes_dwords(uint32_t cols) { return (uint64_t)ACT_PLANES * cols / 4; }
+inline uint64_t act_counts_bytes(uint32_t cols) { return cols / 8; }
+// The broadcast products' workgroups: four 16-row tiles (64 rows) times up
+// to BCAST_MAX_PARTS slices of the row.
+constexpr uint32_t BCAST_MAX_PARTS = 4;
+inline uint32_t bcast_groups(uint32_t rows) { return (rows + 63) / 64; }
+int iris_gemv_bcast_launch(const GemvArgs& a, hipStream_t stream);
+bool iris_gemv_bcast_applies(const GemvArgs& a);
 
 constexpr uint32_t GEMV_SSQ_SLOTS = 256;
 

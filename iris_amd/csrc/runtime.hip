@@ -436,6 +436,16 @@ static int checkpoint_layer(IrisSession* s, const CkptSink* sink, uint32_t l, ui
     return (int)hipEventRecord(sink->events[l], s->stream);
 }
 
+// A one-row product's input as digit planes left by its producer, with the
+// session's k-split scratch (the launch stages the row from x instead where
+// the broadcast product does not apply).
+static void bcast_input(GemvArgs& g, IrisSession* s, const uint32_t* planes, const uint8_t* counts) {
+    g.x_planes = planes;
+    g.x_counts = counts;
+    g.kpart = s->kpart;
+    g.kcount = s->kcount;
+}
+
 // One mistral-dense layer over the session's rows in s->x (positions from
 // *d_pos; the rows' RoPE table already in rope_sc), its output back in s->x.
 // With `slots` (one row), the residual products leave per-tile sums of
@@ -496,6 +506,13 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
         a.window = 0;
         a.planes = s->attn_planes;
         a.scores = s->scores;
+        // One row: the values launch leaves the context row's digit planes
+        // for the O product.
+        const bool ctx_planes = iris_attention_decode_applies(a, rows, s->max_positions);
+        if (ctx_planes) {
+            a.ctx_planes = s->ctx_planes;
+            a.ctx_counts = s->ctx_counts;
+        }
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 3. attended = W_o ctx + x.
         g = GemvArgs{};
@@ -509,6 +526,7 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
         g.residual = s->x;
         g.residual_stride = H;
         if (slots) g.ssq_out = s->ssq_att;
+        if (ctx_planes) bcast_input(g, s, s->ctx_planes, s->ctx_counts);
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 4. gated = mul(silu(W_gate m), W_up m), m = rms_norm(attended).
@@ -528,6 +546,12 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
             g.ssq_in = s->ssq_att;
             g.ssq_n = h_tiles;
         }
+        // One row: the gated row's digit planes too, for the down product.
+        const bool gated_planes = rows == 1;
+        if (gated_planes) {
+            g.out_planes = s->gated_planes;
+            g.out_counts = s->gated_counts;
+        }
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 5. x = W_down gated + attended.
@@ -542,6 +566,7 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
         g.residual = s->attended;
         g.residual_stride = H;
         if (slots) g.ssq_out = s->ssq_x;
+        if (gated_planes) bcast_input(g, s, s->gated_planes, s->gated_counts);
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
     }
@@ -1055,6 +1080,19 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->scores, attn_scores_ints(d.heads, s->k_pos_stride));
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
+    if (d.family != IRIS_FAMILY_GEMMA_DENSE) {
+        auto allocb = [&](void** p, uint64_t bytes) {
+            if (st == hipSuccess) st = hipMalloc(p, (bytes + 15) / 16 * 16);
+        };
+        const uint32_t h_rows = (d.hidden + Q8_TILE_ROWS - 1) / Q8_TILE_ROWS * Q8_TILE_ROWS;
+        allocb((void**)&s->ctx_planes, act_planes_dwords(qw) * 4);
+        allocb((void**)&s->ctx_counts, act_counts_bytes(qw));
+        allocb((void**)&s->gated_planes, act_planes_dwords(m->max_ffn) * 4);
+        allocb((void**)&s->gated_counts, act_counts_bytes(m->max_ffn));
+        allocb((void**)&s->kpart, (uint64_t)BCAST_MAX_PARTS * h_rows * sizeof(int64_t));
+        allocb((void**)&s->kcount, (uint64_t)bcast_groups(d.hidden) * sizeof(uint32_t));
+        if (st == hipSuccess) st = hipMemset(s->kcount, 0, (uint64_t)bcast_groups(d.hidden) * sizeof(uint32_t));
+    }
     if (max_rows > 1) {
         // Per-block scale matrices go through the matrix cores folded.
         for (uint32_t l = 0; l < d.layers && st == hipSuccess; l++)
@@ -1113,6 +1151,12 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->token_limbs);
     hipFree(s->ssq_x);
     hipFree(s->ssq_att);
+    hipFree(s->ctx_planes);
+    hipFree(s->ctx_counts);
+    hipFree(s->gated_planes);
+    hipFree(s->gated_counts);
+    hipFree(s->kpart);
+    hipFree(s->kcount);
     hipFree(s->attn_planes.q);
     hipFree(s->attn_planes.k);
     hipFree(s->attn_planes.v);

@@ -82,6 +82,14 @@ struct IrisSession {
     // the residual products and read by the norms that follow them.
     int64_t *ssq_x = nullptr, *ssq_att = nullptr;
     bool ssq_x_valid = false;  // the last pass left ssq_x for the head's norm
+    // mistral-dense one-row passes: the context and gated rows as digit
+    // planes from their producers (act_planes layout), read by the O and
+    // down products, and those products' k-split scratch (partial sums,
+    // arrival counters zeroed at allocation).
+    uint32_t *ctx_planes = nullptr, *gated_planes = nullptr;
+    uint8_t *ctx_counts = nullptr, *gated_counts = nullptr;
+    int64_t* kpart = nullptr;
+    uint32_t* kcount = nullptr;
     // gemma-dense one-row passes carry each post-norm into the next product:
     // the product's row stays in tmp with its sums of squares in ssq_x, to be
     // rms_norm'ed with norm_w, added to res and scaled by scalar (0 = none).

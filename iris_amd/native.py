@@ -72,6 +72,7 @@ def _declare(L):
         "iris_memcpy_d2h": (C.c_int, [vp, vp, u64]),
         "iris_memcpy_d2d": (C.c_int, [vp, vp, u64]),
         "iris_time_product": (C.c_int, [vp, u32, vp, u32, vp, u32, C.POINTER(C.c_double)]),
+        "iris_time_bcast_product": (C.c_int, [vp, u32, vp, vp, u32, C.POINTER(C.c_double)]),
         "iris_attention_numerics": (C.c_int, [vp, vp, vp, vp, u32, u32, vp, vp, vp]),
         "iris_silu_device": (C.c_int, [vp, u32, vp]),
         "iris_silu_table_device": (C.c_int, [vp, u32, vp]),
