@@ -113,6 +113,7 @@ extern "C" {
     pub fn iris_probe_mfma_i8(random_operands: u32, iterations: u32, tops: *mut f64) -> c_int;
     pub fn iris_probe_handoff(workgroups: u32, round_trip_us: *mut f64, atomic_us: *mut f64, barrier_us: *mut f64)
         -> c_int;
+    pub fn iris_probe_row_latency(flood_waves: u32, vector_us: *mut f64, scalar_us: *mut f64) -> c_int;
     pub fn iris_time_product(
         matrices: *const *const Q8GpuMatrix,
         count: u32,

@@ -183,6 +183,13 @@ int iris_probe_mfma_i8(uint32_t random_operands, uint32_t iterations, double* to
  * microseconds. Every wait is bounded: -4 when one gave up. */
 int iris_probe_handoff(uint32_t workgroups, double* round_trip_us, double* atomic_us, double* barrier_us);
 
+/* The latency of one load a product's activation row needs, issued while
+ * `flood_waves` (0-15) other waves of each CU's workgroup stream a cold
+ * buffer with 16 loads per lane in flight (no counterpart in the reference;
+ * a measurement): the median over one workgroup per CU of a vector load of
+ * a line other workgroups read and of a scalar load, in microseconds. */
+int iris_probe_row_latency(uint32_t flood_waves, double* vector_us, double* scalar_us);
+
 /* ------------------------------------------------------------------------
  * The deterministic token loop, device-resident.
  *

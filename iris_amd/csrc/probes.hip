@@ -146,6 +146,50 @@ __global__ void handoff_barrier_kernel(uint32_t* count, uint64_t* out, uint32_t*
     out[2 * blockIdx.x + 1] = __builtin_amdgcn_s_memrealtime();
 }
 
+// ---- A row load behind the weight stream ----
+// Every workgroup: `flood` waves each keep ROW_FLOOD_LOADS 16-byte loads per
+// lane in flight from their own slice of a cold buffer (a product's weight
+// stream), and one more wave, after ROW_DELAY ticks (the stream under way),
+// times one vector load of a line other workgroups have read (a product's
+// activation row) and one scalar load, each waited for on its own.
+// out[3g]: the vector load's ticks, out[3g + 1]: the scalar load's.
+constexpr uint32_t ROW_FLOOD_LOADS = 16;
+constexpr uint32_t ROW_DELAY = 100;  // ticks of 10 ns
+
+__global__ __launch_bounds__(1024) void row_latency_kernel(const uint4* cold, uint64_t words_per_wave,
+                                                           const uint32_t* hot, uint32_t hot_words, uint64_t* out) {
+    const uint32_t wave = threadIdx.x >> 6, lane = threadIdx.x & 63, flood = blockDim.x / 64 - 1;
+    if (wave < flood) {
+        const uint4* b = cold + ((uint64_t)blockIdx.x * flood + wave) * words_per_wave;
+        uint32_t acc = 0;
+        for (uint64_t i = lane; i + (ROW_FLOOD_LOADS - 1) * 64 < words_per_wave; i += ROW_FLOOD_LOADS * 64) {
+            uint4 v[ROW_FLOOD_LOADS];
+#pragma unroll
+            for (uint32_t u = 0; u < ROW_FLOOD_LOADS; u++) v[u] = b[i + u * 64];
+#pragma unroll
+            for (uint32_t u = 0; u < ROW_FLOOD_LOADS; u++) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        }
+        if (acc == 0x9E3779B9u) out[3 * blockIdx.x + 2] = acc;
+        return;
+    }
+    const uint64_t t = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t < ROW_DELAY) {}
+    const uint32_t off = (blockIdx.x * 64) % (hot_words - 64);
+    const uint32_t* vp = hot + off + lane;
+    const uint32_t* sp = hot + (off + hot_words / 2) % (hot_words - 64);
+    uint32_t v, sv;
+    const uint64_t ta = __builtin_amdgcn_s_memrealtime();
+    asm volatile("global_load_dword %0, %1, off\n\ts_waitcnt vmcnt(0)" : "=v"(v) : "v"(vp) : "memory");
+    const uint64_t tb = __builtin_amdgcn_s_memrealtime();
+    asm volatile("s_load_dword %0, %1, 0x0\n\ts_waitcnt lgkmcnt(0)" : "=s"(sv) : "s"(sp) : "memory");
+    const uint64_t tc = __builtin_amdgcn_s_memrealtime();
+    if (lane == 0) {
+        out[3 * blockIdx.x] = tb - ta;
+        out[3 * blockIdx.x + 1] = tc - tb;
+        if (v + sv == 0x9E3779B9u) out[3 * blockIdx.x + 2] = v;
+    }
+}
+
 template <class Launch>
 int time_launches(Launch&& launch, uint32_t repeats, double* ms_per_launch) {
     hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -267,4 +311,43 @@ extern "C" int iris_probe_handoff(uint32_t workgroups, double* round_trip_us, do
     hipFree(mem);
     if (st != hipSuccess) return (int)st;
     return herr ? IRIS_E_STATE : 0;
+}
+
+extern "C" int iris_probe_row_latency(uint32_t flood_waves, double* vector_us, double* scalar_us) {
+    if (!vector_us || !scalar_us || flood_waves > 15) return IRIS_E_INVALID;
+    const uint32_t wgs = (uint32_t)iris_device_cus();
+    const uint32_t waves = flood_waves + 1;
+    // 1 MB of cold stream per flooding wave, at least 256 MB in all.
+    const uint64_t words_per_wave = flood_waves ? std::max<uint64_t>((256ull << 20) / 16 / ((uint64_t)wgs * flood_waves),
+                                                                   (1ull << 20) / 16)
+                                                : 0;
+    const uint64_t cold_bytes = std::max<uint64_t>(16, words_per_wave * 16 * wgs * flood_waves);
+    constexpr uint32_t HOT_WORDS = 8192;
+    char* mem = nullptr;
+    hipError_t st = hipMalloc((void**)&mem, cold_bytes + HOT_WORDS * 4 + 24ull * wgs);
+    if (st != hipSuccess) return (int)st;
+    const uint4* cold = (const uint4*)mem;
+    uint32_t* hot = (uint32_t*)(mem + cold_bytes);
+    uint64_t* out = (uint64_t*)(mem + cold_bytes + HOT_WORDS * 4);
+    st = hipMemset(mem, 1, cold_bytes + HOT_WORDS * 4);
+    std::vector<uint64_t> h(3 * (size_t)wgs);
+    for (int rep = 0; st == hipSuccess && rep < 3; rep++) {
+        hipLaunchKernelGGL(row_latency_kernel, dim3(wgs), dim3(64 * waves), 0, nullptr, cold, words_per_wave, hot,
+                           HOT_WORDS, out);
+        st = hipGetLastError();
+        if (st == hipSuccess) st = hipDeviceSynchronize();
+    }
+    if (st == hipSuccess) st = hipMemcpy(h.data(), out, h.size() * 8, hipMemcpyDeviceToHost);
+    hipFree(mem);
+    if (st != hipSuccess) return (int)st;
+    std::vector<uint64_t> vt(wgs), sc(wgs);
+    for (uint32_t g = 0; g < wgs; g++) {
+        vt[g] = h[3 * g];
+        sc[g] = h[3 * g + 1];
+    }
+    std::sort(vt.begin(), vt.end());
+    std::sort(sc.begin(), sc.end());
+    *vector_us = (double)vt[wgs / 2] * 0.01;
+    *scalar_us = (double)sc[wgs / 2] * 0.01;
+    return 0;
 }

@@ -375,6 +375,22 @@ def handoff_latencies(sizes=(8, 32, 288, 1024)) -> dict:
     return out
 
 
+def row_latencies(floods=(0, 1, 3, 7)) -> dict:
+    """How long a product's activation-row load takes behind the weight
+    stream: median microseconds of a vector load (the staged products' row
+    path) and of a scalar load (the broadcast products' digit planes) while
+    `floods` other waves of each CU's workgroup keep 16 cold loads per lane
+    in flight."""
+    L = native.lib()
+    out = {}
+    for f in floods:
+        v, sc = C.c_double(), C.c_double()
+        native.check(L.iris_probe_row_latency(f, C.byref(v), C.byref(sc)), "row latency probe")
+        out[f"vector_load_behind_{f}_waves_us"] = round(v.value, 2)
+        out[f"scalar_load_behind_{f}_waves_us"] = round(sc.value, 2)
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description="time the exact decode loop and its GEMV on the GPU")
     ap.add_argument("--steps", type=int, default=PROMPT - 1)
@@ -399,7 +415,8 @@ def main(argv=None):
     ap.add_argument("--gemma", action="store_true", help="with --eager-decode: the Gemma-2B shape")
     ap.add_argument("--peaks", action="store_true",
                     help="only the measured peaks: HBM read stream and int8 MFMA (constant and random operands), "
-                         "and the handoff latencies between workgroups")
+                         "the handoff latencies between workgroups, and a row load's latency behind the "
+                         "weight stream")
     args = ap.parse_args(argv)
     global USE_GRAPH
     if USE_GRAPH and native.kernel_tracer_loaded():
@@ -410,6 +427,7 @@ def main(argv=None):
     if args.peaks:
         print(json.dumps(measured_peaks()), flush=True)
         print(json.dumps(handoff_latencies()), flush=True)
+        print(json.dumps(row_latencies()), flush=True)
         return
     if args.eager_decode:
         print(json.dumps(eager_decode(args.eager_decode, args.gemma)), flush=True)

@@ -81,6 +81,7 @@ def _declare(L):
         "iris_probe_hbm_read": (C.c_int, [vp, u64, u32, C.POINTER(C.c_double)]),
         "iris_probe_mfma_i8": (C.c_int, [u32, u32, C.POINTER(C.c_double)]),
         "iris_probe_handoff": (C.c_int, [u32, C.POINTER(C.c_double), C.POINTER(C.c_double), C.POINTER(C.c_double)]),
+        "iris_probe_row_latency": (C.c_int, [u32, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     }
     for name, (res, args) in sig.items():
         f = getattr(L, name)
