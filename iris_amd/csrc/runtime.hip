@@ -718,6 +718,12 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
         a.window = L.window;
         a.planes = s->attn_planes;
         a.scores = s->scores;
+        // One row: the context row's digit planes too, for the O product.
+        const bool ctx_planes = iris_attention_decode_applies(a, rows, s->max_positions);
+        if (ctx_planes) {
+            a.ctx_planes = s->ctx_planes;
+            a.ctx_counts = s->ctx_counts;
+        }
         RT_CHECK(iris_attention_launch(a, rows, s->max_positions, st));
         // 4. attended = rms_norm(W_o ctx, post_attention) + x  (:879-892)
         g = GemvArgs{};
@@ -729,6 +735,7 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
         g.out = s->tmp;
         g.out_stride = H;
         if (carry) g.ssq_out = s->ssq_x;
+        if (ctx_planes) bcast_input(g, s, s->ctx_planes, s->ctx_counts);
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         if (!carry)
@@ -755,6 +762,12 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
         g.epilogue = EPI_GEGLU;
         g.out = s->gated;
         g.out_stride = L.ffn;
+        // One row: the gated row's digit planes too, for the down product.
+        const bool gated_planes = rows == 1;
+        if (gated_planes) {
+            g.out_planes = s->gated_planes;
+            g.out_counts = s->gated_counts;
+        }
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         // 6. attended = rms_norm(W_down gated, post_ffw) + attended  (finish_mlp :915-929)
@@ -767,6 +780,7 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
         g.out = s->tmp;
         g.out_stride = H;
         if (carry) g.ssq_out = s->ssq_x;
+        if (gated_planes) bcast_input(g, s, s->gated_planes, s->gated_counts);
         with_gemm_space(g, s, rows);
         RT_CHECK(iris_gemv_launch(g, st));
         if (!carry)
@@ -1080,7 +1094,7 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
     alloc(&s->scores, attn_scores_ints(d.heads, s->k_pos_stride));
     alloc(&s->ctx, (size_t)max_rows * qw);
     alloc(&s->gated, (size_t)max_rows * m->max_ffn);
-    if (d.family != IRIS_FAMILY_GEMMA_DENSE) {
+    {
         auto allocb = [&](void** p, uint64_t bytes) {
             if (st == hipSuccess) st = hipMalloc(p, (bytes + 15) / 16 * 16);
         };
