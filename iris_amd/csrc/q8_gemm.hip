@@ -100,6 +100,11 @@ __global__ __launch_bounds__(256) void token_prep_kernel(const GemvArgs a) {
 
 constexpr uint32_t PLANE_KB = GEMM_PLANE_KB;
 
+__global__ __launch_bounds__(256) void fill_ints_kernel(int32_t* p, uint32_t n, int32_t v) {
+    const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
 // The digit planes of one 32-token tile over PLANE_KB k blocks (one k
 // chunk) per workgroup, after the optional rms_norm (mul_sat(mul_sat(v,
 // scale), w)), in the operand layout above, and the digits the chunk's
@@ -274,6 +279,52 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
 // for the gated activations, each gate/up row pair combined in registers);
 // the blocks are parked in LDS as [row][token], then the epilogue runs
 // row-fastest.
+// The block's gated values (parked in LDS, pair p of token tl at
+// sC[p * step * STRIDE + tl]) as the next product's digit planes: each
+// thread takes 16 consecutive pairs of one token (16 bytes of one operand
+// lane per plane, as digit_planes_kernel writes them; tokens past the last
+// of the launch, up to the end of its last 32-token tile, get zero digits),
+// and the digits each 32-token tile needs meet in LDS, then in the launch's
+// counts by atomicMax (the largest wins in any order). A block's pairs lie
+// in one k chunk (its first pair is a multiple of ROWS / 2 <= 256).
+template <class G, uint32_t NTOK>
+__device__ __forceinline__ void gated_planes(const GemvArgs& a, const int32_t* sC, uint32_t rt0, uint32_t tt0,
+                                             uint32_t step) {
+    constexpr uint32_t ROWS = G::RT * 32, STRIDE = NTOK + 1, NG = ROWS / 2 / 16, NTT = NTOK / 32;
+    static_assert(ROWS / 2 <= 32 * PLANE_KB && NTT <= 4, "one k chunk, at most four token tiles");
+    __shared__ int s_need[4];
+    const uint32_t tid = threadIdx.x;
+    const uint32_t K = a.w.rows / 2, KB = K / 32, M = a.tokens, TT = (M + 31) / 32;
+    const size_t lstride = (size_t)TT * KB * FRAG;
+    if (tid < 4) s_need[tid] = 1;
+    __syncthreads();
+    for (uint32_t c = tid; c < NTOK * NG; c += G::THREADS) {
+        const uint32_t tl = c % NTOK, gi = c / NTOK;
+        const uint32_t pair0 = rt0 * 16 + gi * 16, token = tt0 * 32 + tl;
+        if (pair0 >= K || token / 32 >= TT) continue;
+        const bool valid = token < M;
+        uint64_t d[16];
+        int need = 1;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            d[j] = digits5(valid ? sC[(gi * 16 + j) * step * STRIDE + tl] : 0);
+            need = max(need, limbs_needed(d[j]));
+        }
+        int8_t* dst = a.out_gemm_planes + ((size_t)(token / 32) * KB + pair0 / 32) * FRAG +
+                      ((token % 32) + 32 * ((pair0 % 32) / 16)) * 16;
+#pragma unroll
+        for (int l = 0; l < PL_MAX; l++)
+            *(uint4*)(dst + l * lstride) = make_uint4(plane_byte4(d[0], d[1], d[2], d[3], l),
+                                                      plane_byte4(d[4], d[5], d[6], d[7], l),
+                                                      plane_byte4(d[8], d[9], d[10], d[11], l),
+                                                      plane_byte4(d[12], d[13], d[14], d[15], l));
+        atomicMax(&s_need[tl / 32], need);
+    }
+    __syncthreads();
+    const uint32_t chunk = rt0 * 16 / (32 * PLANE_KB);
+    if (tid < NTT && tt0 + tid < TT && rt0 * 16 < K) atomicMax(&a.out_gemm_limbs[M + chunk * TT + tt0 + tid], s_need[tid]);
+}
+
 template <class G, int TTW, class Values>
 __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
                                                Values&& block_values) {
@@ -331,9 +382,9 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
             for (uint32_t u = 0; u < TB; u++) {
                 const uint32_t c = c0 + u * G::THREADS, pl = c % (ROWS / 2), tl = c / (ROWS / 2);
                 const uint32_t pair = rt0 * 16 + pl, token = tt0 * 32 + tl;
-                if (2 * pair < w.rows && token < a.tokens)
-                    a.out[(size_t)token * a.out_stride + pair] =
-                        dn::mul_sat(dn::silu_from_tab(gate[u], looked[u]), up[u]);
+                const int32_t o = dn::mul_sat(dn::silu_from_tab(gate[u], looked[u]), up[u]);
+                if (2 * pair < w.rows && token < a.tokens) a.out[(size_t)token * a.out_stride + pair] = o;
+                if (a.out_gemm_planes) sC[2 * pl * STRIDE + tl] = o;  // this thread's own slot, read above
             }
         }
     } else if (pairs) {
@@ -369,6 +420,7 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
         }
     }
     __syncthreads();
+    if (pairs && a.out_gemm_planes) gated_planes<G, NTOK>(a, sC, rt0, tt0, table ? 2 : 1);
 }
 
 // Row-scale matrices: the planes recombine into the row's integer dot
@@ -743,10 +795,22 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     if (!iris_gemm_applies(a) || a.x_stride % 4 || ((uintptr_t)a.x & 15) || ((uintptr_t)a.planes & 255))
         return IRIS_E_INVALID;
     if (a.prologue == PRO_RMSNORM && ((uintptr_t)a.norm_w & 15)) return IRIS_E_INVALID;
+    if (a.planes_ready && a.prologue != PRO_NONE) return IRIS_E_INVALID;
+    const bool gated = a.epilogue == EPI_SWIGLU || a.epilogue == EPI_GEGLU;
+    if (a.out_gemm_planes && (!gated || !a.out_gemm_limbs || (a.w.rows / 2) % 32 || ((uintptr_t)a.out_gemm_planes & 255) ||
+                              a.out_gemm_planes == a.planes || a.out_gemm_limbs == a.token_limbs))
+        return IRIS_E_INVALID;
     const uint32_t TT = (a.tokens + 31) / 32, KB = a.w.cols / 32;
-    if (a.prologue == PRO_RMSNORM)
-        hipLaunchKernelGGL(token_prep_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
-    hipLaunchKernelGGL(digit_planes_kernel, dim3(TT, (KB + PLANE_KB - 1) / PLANE_KB), dim3(256), 0, stream, a);
+    if (!a.planes_ready) {
+        if (a.prologue == PRO_RMSNORM)
+            hipLaunchKernelGGL(token_prep_kernel, dim3((a.tokens + 3) / 4), dim3(256), 0, stream, a);
+        hipLaunchKernelGGL(digit_planes_kernel, dim3(TT, (KB + PLANE_KB - 1) / PLANE_KB), dim3(256), 0, stream, a);
+    }
+    if (a.out_gemm_planes) {
+        // The gated rows' counts start at 1 (every workgroup raises its own).
+        const uint32_t n = (uint32_t)(gemm_limb_ints(a.w.rows / 2, a.tokens) - a.tokens);
+        hipLaunchKernelGGL(fill_ints_kernel, dim3((n + 255) / 256), dim3(256), 0, stream, a.out_gemm_limbs + a.tokens, n, 1);
+    }
     hipError_t st = hipGetLastError();
     if (st != hipSuccess) return (int)st;
     if (a.w.scale_mode == Q8_SCALE_F16) {

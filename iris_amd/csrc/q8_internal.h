@@ -183,6 +183,17 @@ struct GemvArgs {
     // too (ActPlanes layout over out's row; null: not written).
     uint32_t* out_planes;
     uint8_t* out_counts;
+    // Multi-token EPI_SWIGLU / EPI_GEGLU products on the matrix cores: the
+    // gated rows also as the next product's digit planes (the `planes`
+    // layout over rows / 2 columns, gemm_planes_bytes) and the digits each
+    // (k chunk, 32-token tile) needs (the `token_limbs` layout after the
+    // first `tokens` ints; the launcher sets them to 1 first). Null: not
+    // written.
+    int8_t* out_gemm_planes;
+    int32_t* out_gemm_limbs;
+    // Multi-token PRO_NONE products whose planes and counts are already in
+    // planes / token_limbs (their producer wrote them): no preparation.
+    int planes_ready;
 };
 
 // A row of int32 values as the broadcast products read it: plane l (of

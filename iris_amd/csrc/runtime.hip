@@ -553,22 +553,31 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
             g.out_counts = s->gated_counts;
         }
         with_gemm_space(g, s, rows);
-        RT_CHECK(iris_gemv_launch(g, st));
         // 5. x = W_down gated + attended.
-        g = GemvArgs{};
-        g.w = q8_view(L.wdown);
-        g.x = s->gated;
-        g.x_stride = d.ffn;
-        g.tokens = rows;
-        g.epilogue = EPI_RESIDUAL;
-        g.out = s->x;
-        g.out_stride = H;
-        g.residual = s->attended;
-        g.residual_stride = H;
-        if (slots) g.ssq_out = s->ssq_x;
-        if (gated_planes) bcast_input(g, s, s->gated_planes, s->gated_counts);
-        with_gemm_space(g, s, rows);
+        GemvArgs dn{};
+        dn.w = q8_view(L.wdown);
+        dn.x = s->gated;
+        dn.x_stride = d.ffn;
+        dn.tokens = rows;
+        dn.epilogue = EPI_RESIDUAL;
+        dn.out = s->x;
+        dn.out_stride = H;
+        dn.residual = s->attended;
+        dn.residual_stride = H;
+        if (slots) dn.ssq_out = s->ssq_x;
+        if (gated_planes) bcast_input(dn, s, s->gated_planes, s->gated_counts);
+        with_gemm_space(dn, s, rows);
+        // Several rows, both products on the matrix cores: the gate/up
+        // product writes the gated rows' digit planes for the down product.
+        if (rows > 1 && s->gated_gemm_planes && iris_gemm_applies(g) && iris_gemm_applies(dn)) {
+            g.out_gemm_planes = s->gated_gemm_planes;
+            g.out_gemm_limbs = s->gated_gemm_limbs;
+            dn.planes = s->gated_gemm_planes;
+            dn.token_limbs = s->gated_gemm_limbs;
+            dn.planes_ready = 1;
+        }
         RT_CHECK(iris_gemv_launch(g, st));
+        RT_CHECK(iris_gemv_launch(dn, st));
     }
     return 0;
 }
@@ -769,20 +778,29 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
             g.out_counts = s->gated_counts;
         }
         with_gemm_space(g, s, rows);
-        RT_CHECK(iris_gemv_launch(g, st));
         // 6. attended = rms_norm(W_down gated, post_ffw) + attended  (finish_mlp :915-929)
-        g = GemvArgs{};
-        g.w = q8_view(L.wdown);
-        g.x = s->gated;
-        g.x_stride = L.ffn;
-        g.tokens = rows;
-        g.epilogue = EPI_STORE;
-        g.out = s->tmp;
-        g.out_stride = H;
-        if (carry) g.ssq_out = s->ssq_x;
-        if (gated_planes) bcast_input(g, s, s->gated_planes, s->gated_counts);
-        with_gemm_space(g, s, rows);
+        GemvArgs dn{};
+        dn.w = q8_view(L.wdown);
+        dn.x = s->gated;
+        dn.x_stride = L.ffn;
+        dn.tokens = rows;
+        dn.epilogue = EPI_STORE;
+        dn.out = s->tmp;
+        dn.out_stride = H;
+        if (carry) dn.ssq_out = s->ssq_x;
+        if (gated_planes) bcast_input(dn, s, s->gated_planes, s->gated_counts);
+        with_gemm_space(dn, s, rows);
+        // Several rows, both products on the matrix cores: the gate/up
+        // product writes the gated rows' digit planes for the down product.
+        if (rows > 1 && s->gated_gemm_planes && iris_gemm_applies(g) && iris_gemm_applies(dn)) {
+            g.out_gemm_planes = s->gated_gemm_planes;
+            g.out_gemm_limbs = s->gated_gemm_limbs;
+            dn.planes = s->gated_gemm_planes;
+            dn.token_limbs = s->gated_gemm_limbs;
+            dn.planes_ready = 1;
+        }
         RT_CHECK(iris_gemv_launch(g, st));
+        RT_CHECK(iris_gemv_launch(dn, st));
         if (!carry)
             RT_CHECK(iris_norm_residual_launch(s->tmp, H, L.norm_post_ffw, d.norm_eps, s->attended, H, 0, s->attended,
                                                H, H, rows, st));
@@ -1117,6 +1135,8 @@ int iris_session_create(IrisModel* m, uint32_t max_positions, uint32_t max_rows,
         size_t widest = std::max<size_t>(d.hidden, std::max<size_t>(qw, m->max_ffn));
         if (st == hipSuccess) st = hipMalloc((void**)&s->planes, gemm_planes_bytes((uint32_t)widest, max_rows));
         alloc(&s->token_limbs, (size_t)gemm_limb_ints((uint32_t)widest, max_rows));
+        if (st == hipSuccess) st = hipMalloc((void**)&s->gated_gemm_planes, gemm_planes_bytes(m->max_ffn, max_rows));
+        alloc(&s->gated_gemm_limbs, (size_t)gemm_limb_ints(m->max_ffn, max_rows));
         AttnPlanes& ap = s->attn_planes;
         ap.qt_cap = (max_rows + 15) / 16;
         ap.ks_cap = (max_positions + 63) / 64;
@@ -1163,6 +1183,8 @@ void iris_session_free(IrisSession* s) {
     hipFree(s->sel_partial);
     hipFree(s->planes);
     hipFree(s->token_limbs);
+    hipFree(s->gated_gemm_planes);
+    hipFree(s->gated_gemm_limbs);
     hipFree(s->ssq_x);
     hipFree(s->ssq_att);
     hipFree(s->ctx_planes);

@@ -109,6 +109,10 @@ struct IrisSession {
     int32_t *qkv = nullptr, *tmp = nullptr, *ple_proj = nullptr, *ple_rows = nullptr, *ple_gated = nullptr;
     // digit planes of a multi-row pass's activations for the MFMA products
     int8_t* planes = nullptr;        // gemm_planes_bytes(widest product input, max_rows)
+    // multi-row passes: the gated rows' planes and counts, written by the
+    // gate/up product for the down product
+    int8_t* gated_gemm_planes = nullptr;   // gemm_planes_bytes(max_ffn, max_rows)
+    int32_t* gated_gemm_limbs = nullptr;   // gemm_limb_ints(max_ffn, max_rows)
     const int32_t* silu_tab = nullptr;  // mistral-dense: the device's silu table (not owned)
     int32_t* token_limbs = nullptr;  // [2][max_rows]: digit counts, norm scales
     int32_t *logits = nullptr, *ids = nullptr, *tokens = nullptr;
