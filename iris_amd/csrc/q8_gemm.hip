@@ -199,7 +199,9 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
     static_assert(PER_WAVE * G::WAVES * FRAG <= G::STAGE && PER_WAVE >= 2, "stage layout");
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     // The wave within its k group, the group's ring and k steps [ks0, ks1).
-    const uint32_t half = (tid >> 6) / G::WAVES, wave = (tid >> 6) % G::WAVES;
+    // The k group through readfirstlane: uniform, so the k loop's control
+    // stays in scalar registers.
+    const uint32_t half = __builtin_amdgcn_readfirstlane((tid >> 6) / G::WAVES), wave = (tid >> 6) % G::WAVES;
     const uint32_t wr = wave % (G::WAVES / 2), wt = wave / (G::WAVES / 2);
     const Q8View& w = a.w;
     const uint32_t KS = w.cols / 64, KB = w.cols / 32, TT = (a.tokens + 31) / 32;
