@@ -385,13 +385,14 @@ __device__ __forceinline__ void park_and_store(const GemvArgs& a, int8_t* smem, 
                 const uint32_t c = c0 + u * G::THREADS, pl = c % (ROWS / 2), tl = c / (ROWS / 2);
                 const uint32_t pair = rt0 * 16 + pl, token = tt0 * 32 + tl;
                 const int32_t o = dn::mul_sat(dn::silu_from_tab(gate[u], looked[u]), up[u]);
-                if (2 * pair < w.rows && token < a.tokens) a.out[(size_t)token * a.out_stride + pair] = o;
+                if (a.out && 2 * pair < w.rows && token < a.tokens) a.out[(size_t)token * a.out_stride + pair] = o;
                 if (a.out_gemm_planes) sC[2 * pl * STRIDE + tl] = o;  // this thread's own slot, read above
             }
         }
     } else if (pairs) {
-        // out[token][row / 2] for the block's ROWS / 2 pairs.
-        for (uint32_t c = tid; c < ROWS / 2 * NTOK; c += G::THREADS) {
+        // out[token][row / 2] for the block's ROWS / 2 pairs (none when the
+        // gated rows are kept only as planes).
+        for (uint32_t c = tid; a.out && c < ROWS / 2 * NTOK; c += G::THREADS) {
             const uint32_t pl = c % (ROWS / 2), tl = c / (ROWS / 2);
             const uint32_t pair = rt0 * 16 + pl, token = tt0 * 32 + tl;
             if (2 * pair < w.rows && token < a.tokens) a.out[(size_t)token * a.out_stride + pair] = sC[pl * STRIDE + tl];
@@ -802,6 +803,7 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     if (a.out_gemm_planes && (!gated || !a.out_gemm_limbs || (a.w.rows / 2) % 32 || ((uintptr_t)a.out_gemm_planes & 255) ||
                               a.out_gemm_planes == a.planes || a.out_gemm_limbs == a.token_limbs))
         return IRIS_E_INVALID;
+    if (!a.out && !a.out_gemm_planes) return IRIS_E_INVALID;
     const uint32_t TT = (a.tokens + 31) / 32, KB = a.w.cols / 32;
     if (!a.planes_ready) {
         if (a.prologue == PRO_RMSNORM)

@@ -188,7 +188,8 @@ struct GemvArgs {
     // layout over rows / 2 columns, gemm_planes_bytes) and the digits each
     // (k chunk, 32-token tile) needs (the `token_limbs` layout after the
     // first `tokens` ints; the launcher sets them to 1 first). Null: not
-    // written.
+    // written. With them, `out` may be null: the gated rows are then kept
+    // only as planes.
     int8_t* out_gemm_planes;
     int32_t* out_gemm_limbs;
     // Multi-token PRO_NONE products whose planes and counts are already in

@@ -570,6 +570,7 @@ static int mistral_layer(IrisSession* s, uint32_t l, uint32_t rows, bool slots, 
         // Several rows, both products on the matrix cores: the gate/up
         // product writes the gated rows' digit planes for the down product.
         if (rows > 1 && s->gated_gemm_planes && iris_gemm_applies(g) && iris_gemm_applies(dn)) {
+            g.out = nullptr;  // nothing reads the gated rows themselves
             g.out_gemm_planes = s->gated_gemm_planes;
             g.out_gemm_limbs = s->gated_gemm_limbs;
             dn.planes = s->gated_gemm_planes;
@@ -793,6 +794,7 @@ static int gemma_layer(IrisSession* s, uint32_t l, uint32_t rows, bool carry) {
         // Several rows, both products on the matrix cores: the gate/up
         // product writes the gated rows' digit planes for the down product.
         if (rows > 1 && s->gated_gemm_planes && iris_gemm_applies(g) && iris_gemm_applies(dn)) {
+            g.out = nullptr;  // nothing reads the gated rows themselves
             g.out_gemm_planes = s->gated_gemm_planes;
             g.out_gemm_limbs = s->gated_gemm_limbs;
             dn.planes = s->gated_gemm_planes;
