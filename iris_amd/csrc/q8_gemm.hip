@@ -180,6 +180,25 @@ __device__ __forceinline__ void wait_vmem() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+// 16 bytes per lane from src into LDS at byte offset lds (the wave's base,
+// the same in every lane; lane i writes lds + 16i): global_load_lds_dwordx4.
+// Written out here because the compiler, lacking alias information, treats
+// every copy still in flight as a write to any LDS address a later ds_read
+// touches, and in some shapes waited for all of them (vmcnt(0)) before each
+// k step's reads, so the next step's copies, issued just before, no longer
+// overlapped the step's matrix work. The k loops' own waits (wait_vmem, then
+// the barrier) order each copy before the reads of its stage, and the
+// compiler's waits for its own loads stay correct: the copies only make its
+// vmcnt counts more conservative.
+__device__ __forceinline__ void copy_to_lds16(const int8_t* src, uint32_t lds) {
+    asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "{m0}"(__builtin_amdgcn_readfirstlane(lds))
+                 : "memory");
+}
+
+// The LDS byte offset of a pointer into LDS: a flat address of LDS is the
+// aperture above the offset, so its low 32 bits.
+__device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t)(uintptr_t)p; }
+
 // One pass of the workgroup over the whole k range: RT weight tiles of 32
 // rows (from 32-row tile rt0) times 2*TTW token tiles of 32 (from tt0) times
 // LG digit planes. Wave (wr, wt) accumulates weight tiles wr*2, wr*2+1
@@ -228,13 +247,12 @@ __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, u
             src[i] = a.planes + l * lstride + ((size_t)tile * KB + sub) * FRAG + lane * 16;
         }
     }
+    const uint32_t ring = lds_offset(smem);
     auto issue = [&](uint32_t ks) {
-        int8_t* base = smem + (ks % GM_STAGES) * GM_STAGE;
+        const uint32_t base = ring + (ks % GM_STAGES) * GM_STAGE;
 #pragma unroll
         for (uint32_t i = 0; i < PER_WAVE; i++)
-            __builtin_amdgcn_global_load_lds(src[i] + (size_t)ks * step[i],
-                                             (__attribute__((address_space(3))) void*)(base + (wave + G::WAVES * i) * FRAG),
-                                             16, 0, 0);
+            copy_to_lds16(src[i] + (size_t)ks * step[i], base + (wave + G::WAVES * i) * FRAG);
     };
 
 #pragma unroll
@@ -692,13 +710,12 @@ __device__ __forceinline__ void fold_mainloop(const GemvArgs& a, int8_t* smem, u
             step[i] = 2 * FRAG;
         }
     }
+    const uint32_t ring = lds_offset(smem);
     auto issue = [&](uint32_t ks) {
-        int8_t* base = smem + (ks % STAGES) * STAGE;
+        const uint32_t base = ring + (ks % STAGES) * STAGE;
 #pragma unroll
         for (uint32_t i = 0; i < PER_WAVE; i++)
-            __builtin_amdgcn_global_load_lds(src[i] + (size_t)ks * step[i],
-                                             (__attribute__((address_space(3))) void*)(base + (wave + G::WAVES * i) * FRAG),
-                                             16, 0, 0);
+            copy_to_lds16(src[i] + (size_t)ks * step[i], base + (wave + G::WAVES * i) * FRAG);
     };
 #pragma unroll
     for (uint32_t s = 0; s < STAGES - 1; s++)
