@@ -849,7 +849,10 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
         return (int)hipGetLastError();
     }
     // Two waves per SIMD and 256 rows x 128 tokens when that still gives
-    // every CU a workgroup, else one wave per SIMD and 128 rows, with 64
+    // every CU a workgroup in at most half the rounds of the 128-row shape
+    // (whose workgroups do half the work: q/k/v at 2048 tokens, 384 of the
+    // larger against 768 of the smaller, 2048-row pass 69.35 -> 69.17 ms),
+    // else one wave per SIMD and 128 rows, with 64
     // tokens when the rounds of workgroups that gives cost less: a 64-token
     // workgroup takes about 2/3 of a 128-token one's time (M=512, K=N=4096:
     // 256 of them 60.6 us, 128 of the larger 92.1 us).
@@ -857,11 +860,11 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     const uint32_t cus = (uint32_t)iris_device_cus();
     const uint32_t n8 = (a.w.tiles + 15) / 16 * n_tg, n4 = (a.w.tiles + 7) / 8 * n_tg;
     const uint32_t n42 = (a.w.tiles + 7) / 8 * n_tg2;
-    const uint32_t rounds4 = (n4 + cus - 1) / cus, rounds2 = (n42 + cus - 1) / cus;
+    const uint32_t rounds8 = (n8 + cus - 1) / cus, rounds4 = (n4 + cus - 1) / cus, rounds2 = (n42 + cus - 1) / cus;
     // The four-wave shapes split the k steps between two wave groups when
     // there is an even number of them (both groups' barriers pair up).
     const bool split = (a.w.cols / 64) % 2 == 0;
-    if (n8 >= cus)
+    if (n8 >= cus && (2 * rounds8 <= rounds4 || !split))
         hipLaunchKernelGGL((q8_gemm_row_kernel<8, 4>), dim3(n8), dim3(512), 0, stream, a);
     else if (n42 != n4 && 2 * rounds2 <= 3 * rounds4) {
         if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2, 2>), dim3(n42), dim3(512), 0, stream, a);
