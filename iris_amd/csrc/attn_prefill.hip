@@ -249,7 +249,16 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
     uint32_t* estore = p.e_store + ((size_t)head * p.qt_cap + qt) * p.ks_cap * 4 * 256 + lane * 4;
     int32_t best = INT32_MIN;
     uint32_t best_key = 0xffffffffu;
-    if constexpr (KEY_PREFETCH) load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+    if constexpr (KEY_PREFETCH) {
+        load_key_tile<HD, LQK>(kbase + (size_t)kt0 * DS * FRAG, kl, kf);
+        // Waited for here, where the compiler sees it (s_waitcnt vmcnt(0)):
+        // a load into kf still pending at the loop's entry made its wait
+        // insertion, which merges the loop's entry with its back edge,
+        // wait for every load before each tile's products, the next tile's
+        // prefetch included. With none pending, each tile waits for its
+        // prefetch only where kn is copied into kf, after its products.
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+    }
 #pragma unroll 1
     for (uint32_t kt = kt0; kt < kt1; kt++) {
         if constexpr (KEY_PREFETCH) {
@@ -290,6 +299,10 @@ __device__ __forceinline__ void prefill_wave(const AttnArgs& a, uint32_t tokens,
     // term is below 2^32 - 2^15).
     uint64_t sum = 0;
     uint4 sn = *(const uint4*)(estore + (size_t)kt0 * 256);
+    // Waited for here, visibly (as the first key tile above): otherwise
+    // each tile's wait for its prefetched scores also covered the previous
+    // tile's store of its terms.
+    __builtin_amdgcn_s_waitcnt(0x0f70);
 #pragma unroll 1
     for (uint32_t kt = kt0; kt < kt1; kt++) {
         const uint4 scv = sn;
