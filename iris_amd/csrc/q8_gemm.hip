@@ -208,14 +208,24 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) { return (uint32_t
 // tile j at 2RT + 2(l * 2TTW + j) + s (padded to a whole number of chunks
 // per wave with copies of chunk 0). Operands past the last tile are clamped
 // onto it (read, never stored).
-template <class G, int LG, int TTW>
+template <class G, int LG, int TTW, bool DEEP = false>
 __device__ __forceinline__ void gemm_mainloop(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0,
                                               v16i (&acc)[2][TTW][LG]) {
     constexpr uint32_t TTWG = 2 * TTW;                      // token tiles per pass
     constexpr uint32_t CHUNKS = 2 * G::RT + 2 * LG * TTWG;  // 1 KB operands per stage
     constexpr uint32_t PER_WAVE = (CHUNKS + G::WAVES - 1) / G::WAVES;
-    constexpr uint32_t GM_RT = G::RT, GM_STAGES = G::STAGES, GM_STAGE = G::STAGE;
     static_assert(PER_WAVE * G::WAVES * FRAG <= G::STAGE && PER_WAVE >= 2, "stage layout");
+    // The ring's stages are as large as this pass's operands, so fewer
+    // digit planes leave room for more stages in the same LDS: four where
+    // four fit, else the shape's own count; with DEEP (long rows), as many
+    // as fit up to four. At three planes and 64 tokens the split four-wave
+    // shape then runs three stages instead of two: faster over the 112 k
+    // steps of a K=14336 down product (the 512-row prompt pass 20.1-20.2 ->
+    // 19.6-19.75 ms), slower over K=4096 (the M=512 product 48.4 -> 49.6 us).
+    constexpr uint32_t GM_RT = G::RT, GM_STAGE = PER_WAVE * G::WAVES * FRAG;
+    constexpr uint32_t FIT = G::RING / GM_STAGE;
+    constexpr uint32_t GM_STAGES = FIT >= 4 ? 4 : DEEP && FIT > G::STAGES ? FIT : G::STAGES;
+    static_assert(GM_STAGES * GM_STAGE <= G::RING, "ring layout");
     const uint32_t tid = threadIdx.x, lane = tid & 63;
     // The wave within its k group, the group's ring and k steps [ks0, ks1).
     // The k group through readfirstlane: uniform, so the k loop's control
@@ -481,7 +491,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemvArgs& a, int8_t* smem, u
     });
 }
 
-template <class G, int LG, int TTW>
+template <class G, int LG, int TTW, bool DEEP>
 __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint32_t rt0, uint32_t tt0) {
     v16i acc[2][TTW][LG];
 #pragma unroll
@@ -490,7 +500,7 @@ __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint3
         for (int j = 0; j < TTW; j++)
 #pragma unroll
             for (int l = 0; l < LG; l++) acc[i][j][l] = v16i{};
-    gemm_mainloop<G, LG, TTW>(a, smem, rt0, tt0, acc);
+    gemm_mainloop<G, LG, TTW, DEEP>(a, smem, rt0, tt0, acc);
     if constexpr (G::SPLITS == 2) {
         // The second k group's sums into the first's, one row tile at a
         // time through LDS (TTW * LG * 16 KB each), lane-contiguous.
@@ -531,7 +541,7 @@ __device__ __forceinline__ void gemm_pass(const GemvArgs& a, int8_t* smem, uint3
 // contiguous range, walked in bands of 8 row groups with the token groups
 // inside a band, so blocks in flight together share operands in their XCD's
 // L2.
-template <uint32_t W, uint32_t TG, uint32_t SPLIT = 1>
+template <uint32_t W, uint32_t TG, uint32_t SPLIT = 1, bool DEEP = false>
 __global__ __launch_bounds__(64 * W * SPLIT, 1) void q8_gemm_row_kernel(const GemvArgs a) {
     static_assert(TG == 2 || TG == 4, "64 or 128 tokens per workgroup");
     using G = GemmShape<W, SPLIT>;
@@ -550,16 +560,16 @@ __global__ __launch_bounds__(64 * W * SPLIT, 1) void q8_gemm_row_kernel(const Ge
     const int limbs = tiles_limbs(a, tt0, TG, s_limbs);
     constexpr int TTW = TG / 2;  // token tiles per wave for up to three planes
     switch (limbs) {
-        case 1: gemm_pass<G, 1, TTW>(a, smem, rt0, tt0); break;
-        case 2: gemm_pass<G, 2, TTW>(a, smem, rt0, tt0); break;
-        case 3: gemm_pass<G, 3, TTW>(a, smem, rt0, tt0); break;
+        case 1: gemm_pass<G, 1, TTW, DEEP>(a, smem, rt0, tt0); break;
+        case 2: gemm_pass<G, 2, TTW, DEEP>(a, smem, rt0, tt0); break;
+        case 3: gemm_pass<G, 3, TTW, DEEP>(a, smem, rt0, tt0); break;
         case 4:
-            gemm_pass<G, 4, 1>(a, smem, rt0, tt0);
-            if constexpr (TG == 4) gemm_pass<G, 4, 1>(a, smem, rt0, tt0 + 2);
+            gemm_pass<G, 4, 1, DEEP>(a, smem, rt0, tt0);
+            if constexpr (TG == 4) gemm_pass<G, 4, 1, DEEP>(a, smem, rt0, tt0 + 2);
             break;
         default:
-            gemm_pass<G, 5, 1>(a, smem, rt0, tt0);
-            if constexpr (TG == 4) gemm_pass<G, 5, 1>(a, smem, rt0, tt0 + 2);
+            gemm_pass<G, 5, 1, DEEP>(a, smem, rt0, tt0);
+            if constexpr (TG == 4) gemm_pass<G, 5, 1, DEEP>(a, smem, rt0, tt0 + 2);
             break;
     }
 }
@@ -864,13 +874,17 @@ int iris_gemm_launch(const GemvArgs& a, hipStream_t stream) {
     // The four-wave shapes split the k steps between two wave groups when
     // there is an even number of them (both groups' barriers pair up).
     const bool split = (a.w.cols / 64) % 2 == 0;
+    // Deeper rings for long rows (at least 64 k steps per wave group).
+    const bool deep = a.w.cols >= 8192;
     if (n8 >= cus && (2 * rounds8 <= rounds4 || !split))
         hipLaunchKernelGGL((q8_gemm_row_kernel<8, 4>), dim3(n8), dim3(512), 0, stream, a);
     else if (n42 != n4 && 2 * rounds2 <= 3 * rounds4) {
-        if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2, 2>), dim3(n42), dim3(512), 0, stream, a);
+        if (split && deep) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2, 2, true>), dim3(n42), dim3(512), 0, stream, a);
+        else if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2, 2>), dim3(n42), dim3(512), 0, stream, a);
         else hipLaunchKernelGGL((q8_gemm_row_kernel<4, 2>), dim3(n42), dim3(256), 0, stream, a);
     } else {
-        if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4, 2>), dim3(n4), dim3(512), 0, stream, a);
+        if (split && deep) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4, 2, true>), dim3(n4), dim3(512), 0, stream, a);
+        else if (split) hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4, 2>), dim3(n4), dim3(512), 0, stream, a);
         else hipLaunchKernelGGL((q8_gemm_row_kernel<4, 4>), dim3(n4), dim3(256), 0, stream, a);
     }
     return (int)hipGetLastError();

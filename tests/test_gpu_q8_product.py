@@ -208,15 +208,17 @@ def grouped_activations(rng, tokens, cols):
 
 
 @pytest.mark.parametrize("tokens,rows,cols", [(603, 1024, 192), (603, 136, 4160), (300, 272, 64), (300, 22100, 128),
-                                              (200, 32768, 64), (603, 1024, 256), (603, 136, 4224)])
+                                              (200, 32768, 64), (603, 1024, 256), (603, 136, 4224),
+                                              (603, 136, 8192)])
 def test_mfma_product_digit_paths(tokens, rows, cols):
     # Every digit count's code path (one to three planes side by side, four
     # and five in two token halves), one-step, short and long k loops,
     # launches whose block count does and does not split evenly over the
     # XCDs, and both workgroup shapes (256-row blocks when the launch fills
     # every CU: the fourth and fifth cases). The 128-row shapes split an
-    # even number of 64-wide k steps between two wave groups (the last two
-    # cases) and walk an odd number in one (the first three).
+    # even number of 64-wide k steps between two wave groups (the last three
+    # cases; rows of 8192 or more take the deeper rings, three stages at
+    # three planes) and walk an odd number in one (the first three).
     rng = np.random.default_rng(tokens + rows + cols)
     raw = synth.q8_matrix(synth.tensor_seed(11, rows), rows, cols, synth.scale_base_for(cols), True)
     m = Q8Matrix.from_bytes(raw, rows, cols)
